@@ -1,0 +1,88 @@
+/* inferop (MI355X build) : C-ABI of the blockwise-FP8 W8A8 path.
+ *
+ * The flat, FFI-friendly form of the C++ API in inferop/ops.h (ctypes, cgo,
+ * JNI or N-API bind these).  Same argument meaning and the same no-op and
+ * error behaviour as the C++ functions; in addition each call returns a
+ * status code.  Plain C types only: tensors are device pointers, dtypes are
+ * the int32 values of inferop::dtype (0 fp32, 1 fp16, 2 bf16, 3 fp8_e4m3),
+ * the stream is a hipStream_t passed as void* (NULL = null stream).
+ *
+ * Each entry point names the reference interface it replaces
+ * (TheonHuang/Inference, include/inferop/ops.h).
+ */
+#ifndef INFEROP_C_H
+#define INFEROP_C_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  INFEROP_OK = 0,
+  INFEROP_ERR_SHAPE = 1,     /* rejected shape: the call did nothing */
+  INFEROP_ERR_DTYPE = 2,     /* unsupported dtype: the call did nothing */
+  INFEROP_ERR_DEVICE = 3,    /* no HIP device / unsupported architecture */
+  INFEROP_ERR_LAUNCH = 4,    /* the HIP runtime reported an error */
+  INFEROP_ERR_ARGUMENT = 5   /* invalid argument of a tuning entry point */
+};
+
+/* Human-readable text of a status code. */
+const char* inferop_status_string(int status);
+
+/* --- introspection: replaces ops.h:19-25 --- */
+int inferop_has_device(void);                 /* has_cuda() */
+int inferop_device_count(void);               /* device_count() */
+const char* inferop_device_name(int ordinal); /* device_name(int) */
+int inferop_device_arch(int ordinal);         /* device_sm_version(int): gfx number, e.g. 950 */
+
+/* --- replaces ops.h:64-65 quant_fp8_per_token_group ---
+ * Shapes with rows <= 0, cols <= 0, group_size <= 0 or cols % group_size != 0
+ * return INFEROP_ERR_SHAPE; dt outside {fp32, fp16, bf16} returns
+ * INFEROP_ERR_DTYPE; in both cases nothing is written (the reference's
+ * silent no-op). */
+int inferop_quant_fp8_per_token_group(void* q, void* scales, const void* x, int32_t dt,
+                                      int64_t rows, int64_t cols, int32_t group_size,
+                                      void* stream);
+
+/* --- replaces ops.h:68-70 dequant_fp8_per_token_group --- same guards. */
+int inferop_dequant_fp8_per_token_group(void* x, int32_t dt, const void* q, const void* scales,
+                                        int64_t rows, int64_t cols, int32_t group_size,
+                                        void* stream);
+
+/* --- replaces ops.h:81-84 w8a8_block_fp8_gemm ---
+ * group_size != 128, block_n != 128, k % 128 != 0, m <= 0 or n <= 0 print the
+ * reference's one-line diagnostic to stderr and return INFEROP_ERR_SHAPE;
+ * out_dt outside {fp32, fp16, bf16} returns INFEROP_ERR_DTYPE silently. */
+int inferop_w8a8_block_fp8_gemm(void* c, const void* a_q, const void* a_scales, const void* b_q,
+                                const void* b_scales, int64_t m, int64_t n, int64_t k,
+                                int32_t group_size, int32_t block_n, int32_t out_dt,
+                                void* stream);
+
+/* --- tuning and testing (no counterpart in the reference) ---
+ * The GEMM with an explicit kernel configuration and split-K factor instead
+ * of the automatic gfx950 choice.  config in [0, inferop_gemm_num_configs()). */
+int inferop_gemm_num_configs(void);
+const char* inferop_gemm_config_name(int config);
+int inferop_w8a8_block_fp8_gemm_config(void* c, const void* a_q, const void* a_scales,
+                                       const void* b_q, const void* b_scales, int64_t m,
+                                       int64_t n, int64_t k, int32_t out_dt, int32_t config,
+                                       int32_t split_k, void* stream);
+/* The configuration and split-K factor the automatic choice would use. */
+int inferop_gemm_select(int64_t m, int64_t n, int64_t k, int32_t* config, int32_t* split_k);
+
+/* --- diagnostics (no counterpart in the reference) ---
+ * Compares, on the current device, the hardware E4M3 conversions the fast
+ * paths use with the reference-semantics software codec, for every fp32 bit
+ * pattern in [lo, hi) (hi <= 2^32).  counts: 4 device uint64, zeroed by the
+ * caller: [0] mismatches inside the quantizer fast-path domain (finite,
+ * |v| < 464), [1] mismatches outside it, [2] checksum of the software codes,
+ * [3] decode mismatches over the 256 bytes. */
+int inferop_selftest_fp8_codec(uint64_t lo, uint64_t hi, uint64_t* counts, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

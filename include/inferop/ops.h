@@ -1,0 +1,60 @@
+// inferop (MI355X build) : public host API for the blockwise-FP8 W8A8 path.
+//
+// Drop-in for the reference header include/inferop/ops.h.  Every declaration
+// below has the reference's exact C++ signature and default arguments, so the
+// Itanium-mangled symbols exported by libinferop.so are the ones a program
+// built against the reference links to.  Only the FP8 path is provided
+// (quantizer, dequantizer, blockwise GEMM) plus device introspection.
+//
+// All tensors are caller-owned device pointers.  `stream` is an opaque
+// hipStream_t; nullptr is the null stream.  Calls are asynchronous on that
+// stream, never allocate caller-visible memory and never throw.  Errors follow
+// the reference: invalid quantizer shapes or dtypes are silent no-ops; invalid
+// GEMM shapes print one line to stderr and return; an unsupported GEMM output
+// dtype is a silent no-op.  The C-ABI in inferop/inferop_c.h exposes the same
+// calls with a status code.
+#pragma once
+
+#include "inferop/common.h"
+
+namespace inferop {
+
+// --- device introspection (reference ops.h:19-25) ---------------------------
+// True if at least one HIP device is visible and the kernels are built in.
+bool has_cuda();
+// Number of visible HIP devices (0 when none).
+int device_count();
+// Marketing name of a device, "-" for an invalid ordinal.
+const char* device_name(int ordinal = 0);
+// GPU architecture number of a device, parsed from its gcnArchName
+// ("gfx950" -> 950); -1 for an invalid ordinal.  The reference returns the
+// CUDA SM version here (major*10+minor); callers use it only to compare.
+int device_sm_version(int ordinal = 0);
+
+// --- per-token-group FP8 quantization (reference ops.h:57-65) ---------------
+//   x:      [rows, cols] in dt (fp32 / fp16 / bf16)
+//   q:      [rows, cols] uint8 (E4M3)
+//   scales: [rows, cols / group_size] fp32
+//   absmax = max |x| over the group (NaN ignored)
+//   scale  = absmax == 0 ? 1 : absmax * fl32(1/448)
+//   q      = e4m3_rn_sat(x / scale)   (IEEE division)
+void quant_fp8_per_token_group(void* q, void* scales, const void* x, dtype dt, int64_t rows,
+                               int64_t cols, int group_size = 128, void* stream = nullptr);
+
+// Inverse: x = dt(e4m3_to_float(q) * scale)  (reference ops.h:67-70).
+void dequant_fp8_per_token_group(void* x, dtype dt, const void* q, const void* scales,
+                                 int64_t rows, int64_t cols, int group_size = 128,
+                                 void* stream = nullptr);
+
+// --- W8A8 blockwise-FP8 GEMM (reference ops.h:72-84) ------------------------
+//   C[m,n] = sum_k A_q[m,k] * sa[m, k/128] * B_q[n,k] * sb[n/128, k/128]
+//   A_q: [M,K] E4M3, sa: [M, K/128] fp32          (per-token-group scales)
+//   B_q: [N,K] E4M3, sb: [ceil(N/128), K/128] fp32 (per 128x128 weight block)
+//   C:   [M,N] in out_dt (fp32 / fp16 / bf16)
+// Requires group_size == block_n == 128 and K % 128 == 0; any M, N > 0.
+void w8a8_block_fp8_gemm(void* c, const void* a_q, const void* a_scales, const void* b_q,
+                         const void* b_scales, int64_t m, int64_t n, int64_t k,
+                         int group_size = 128, int block_n = 128, dtype out_dt = dtype::bf16,
+                         void* stream = nullptr);
+
+}  // namespace inferop

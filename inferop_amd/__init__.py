@@ -1,0 +1,12 @@
+"""inferop_amd: MI355X-native (gfx950) blockwise-FP8 W8A8 path of inferop.
+
+The product is libinferop.so: the drop-in C++ API of include/inferop/ops.h,
+its C-ABI twin include/inferop/inferop_c.h, and the HIP kernels behind them.
+This package builds it (``inferop_amd.build``) and binds its C-ABI from
+Python (``inferop_amd.ops``, same names as the reference's operators).
+"""
+from ._lib import LIB_PATH, LibraryNotBuilt, lib  # noqa: F401
+from .ops import (  # noqa: F401
+    InferopError, Status, dequant_fp8_per_token_group, dequantize, device_count, device_name,
+    device_sm_version, dtype, gemm, gemm_config_name, gemm_num_configs, gemm_select, has_cuda,
+    quant_fp8_per_token_group, quantize, w8a8_block_fp8_gemm, w8a8_block_fp8_gemm_config)

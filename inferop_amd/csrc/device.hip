@@ -1,0 +1,111 @@
+// Device introspection and the on-device self-test of the E4M3 conversions.
+#include <stdio.h>
+#include <string.h>
+
+#include "device_common.h"
+#include "hip_launch.h"
+
+using namespace inferop_hip;
+
+extern "C" int inferop_hip_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n < 0) return 0;
+  return n;
+}
+
+extern "C" int inferop_hip_current_device(int* ordinal) { return hipGetDevice(ordinal); }
+
+extern "C" int inferop_hip_device_info(int ordinal, char* name, int name_len, int* arch,
+                                       int* cu_count) {
+  hipDeviceProp_t p;
+  hipError_t e = hipGetDeviceProperties(&p, ordinal);
+  if (e != hipSuccess) return e;
+  if (name && name_len > 0) snprintf(name, (size_t)name_len, "%s", p.name);
+  if (arch) {
+    // gcnArchName looks like "gfx950:sramecc+:xnack-"; its digits read as
+    // hexadecimal (gfx950 -> 0x950, gfx90a -> 0x90a).
+    int v = -1;
+    if (strncmp(p.gcnArchName, "gfx", 3) == 0) {
+      v = 0;
+      for (const char* s = p.gcnArchName + 3; *s && *s != ':'; ++s) {
+        if (*s >= '0' && *s <= '9') v = v * 16 + (*s - '0');
+        else if (*s >= 'a' && *s <= 'f') v = v * 16 + (*s - 'a' + 10);
+        else break;
+      }
+    }
+    *arch = v;
+  }
+  if (cu_count) *cu_count = p.multiProcessorCount;
+  return hipSuccess;
+}
+
+namespace {
+
+// One fp32 bit pattern per thread.  Per-block partial results are combined
+// with one 64-bit atomic per block and counter.
+__global__ __launch_bounds__(256) void codec_selftest_kernel(uint64_t lo, uint64_t hi,
+                                                             unsigned long long* counts) {
+  __shared__ unsigned long long s_in, s_out, s_sum;
+  if (threadIdx.x == 0) {
+    s_in = 0;
+    s_out = 0;
+    s_sum = 0;
+  }
+  __syncthreads();
+  unsigned long long in_dom = 0, out_dom = 0, sum = 0;
+  const uint64_t stride = (uint64_t)gridDim.x * 256 * 4;
+  for (uint64_t base = lo + ((uint64_t)blockIdx.x * 256 + threadIdx.x) * 4; base < hi; base += stride) {
+    float v[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) v[t] = u2f((uint32_t)(base + t < hi ? base + t : base));
+    const uint32_t hw = cvt_pk4_e4m3(v[0], v[1], v[2], v[3]);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint64_t i = base + t;
+      if (i >= hi) break;
+      const uint32_t sw = sw_e4m3(v[t]);
+      const uint32_t hb = (hw >> (8 * t)) & 0xFFu;
+      const uint32_t a = f2u(v[t]) & 0x7FFFFFFFu;
+      const bool domain = a < 0x43E80000u;  // finite and |v| < 464
+      if (hb != sw) {
+        if (domain) ++in_dom;
+        else ++out_dom;
+      }
+      sum += (unsigned long long)sw * (unsigned long long)(uint32_t)(i * 2654435761ull);
+    }
+  }
+  atomicAdd(&s_in, in_dom);
+  atomicAdd(&s_out, out_dom);
+  atomicAdd(&s_sum, sum);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    atomicAdd(counts + 0, s_in);
+    atomicAdd(counts + 1, s_out);
+    atomicAdd(counts + 2, s_sum);
+  }
+}
+
+__global__ void decode_selftest_kernel(unsigned long long* counts) {
+  const uint32_t b = threadIdx.x;  // 256 threads: one byte each
+  const f32x2 hw = cvt_pk2_e4m3_f32<false>(b);
+  const float sw = inferop::fp8::e4m3_to_float((uint8_t)b);
+  const bool same = (hw.x != hw.x) ? (sw != sw) : (f2u(hw.x) == f2u(sw));
+  if (!same) atomicAdd(counts + 3, 1ull);
+}
+
+}  // namespace
+
+extern "C" int inferop_hip_selftest_fp8_codec(uint64_t lo, uint64_t hi, uint64_t* counts,
+                                              void* stream) {
+  if (hi > (1ull << 32) || lo > hi || !counts) return hipErrorInvalidValue;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const uint64_t n = hi - lo;
+  uint64_t blocks = (n + 1023) / 1024;
+  if (blocks > 65536) blocks = 65536;
+  if (blocks == 0) blocks = 1;
+  hipLaunchKernelGGL(codec_selftest_kernel, dim3((unsigned)blocks), dim3(256), 0, st, lo, hi,
+                     (unsigned long long*)counts);
+  hipLaunchKernelGGL(decode_selftest_kernel, dim3(1), dim3(256), 0, st,
+                     (unsigned long long*)counts);
+  return hipGetLastError();
+}

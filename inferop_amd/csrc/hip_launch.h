@@ -1,0 +1,69 @@
+/* Thin internal C-ABI between the C++ front end (ops.cpp, built with g++ and
+ * no HIP headers) and the HIP translation units (built with hipcc for
+ * gfx950).  Plain C types only; every launch function returns a hipError_t
+ * value as int (0 = hipSuccess).  Arguments are assumed validated by the
+ * caller (shapes, dtypes); the launch functions only check what the kernels
+ * themselves assume (alignment, grid limits). */
+#ifndef INFEROP_HIP_LAUNCH_H
+#define INFEROP_HIP_LAUNCH_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- device introspection ---- */
+int inferop_hip_device_count(void);
+/* name (NUL-terminated, truncated to name_len), arch number (the gfx digits
+ * read as hexadecimal: gfx950 -> 0x950),
+ * CU count.  Returns hipError_t. */
+int inferop_hip_device_info(int ordinal, char* name, int name_len, int* arch, int* cu_count);
+int inferop_hip_current_device(int* ordinal);
+
+/* ---- quantizer / dequantizer (dt: 0 fp32, 1 fp16, 2 bf16) ---- */
+int inferop_hip_quant_fp8_group(void* q, float* scales, const void* x, int32_t dt, int64_t rows,
+                                int64_t cols, int32_t group_size, void* stream);
+int inferop_hip_dequant_fp8_group(void* x, int32_t dt, const uint8_t* q, const float* scales,
+                                  int64_t rows, int64_t cols, int32_t group_size, void* stream);
+
+/* ---- blockwise FP8 GEMM ----
+ * cfg: index into the kernel table (inferop_hip_gemm_num_configs());
+ * split_k: number of K partitions (1 = none); partitions > 1 reduce through
+ * a library-owned fp32 workspace with a last-arriving-block fixup. */
+typedef struct {
+  int32_t cfg;
+  int32_t split_k;
+} inferop_gemm_launch;
+
+typedef struct {
+  int32_t bn;     /* block tile along N */
+  int32_t bm;     /* block tile along M */
+  int32_t waves;  /* waves per workgroup */
+  int32_t kind;   /* 0 = register-staged LDS pipeline, 1 = direct-to-LDS pipeline */
+  const char* name;
+} inferop_gemm_cfg_info;
+
+int inferop_hip_gemm_num_configs(void);
+int inferop_hip_gemm_config_info(int32_t cfg, inferop_gemm_cfg_info* info);
+int inferop_hip_gemm_w8a8_block(void* c, const uint8_t* a_q, const float* a_scales,
+                                const uint8_t* b_q, const float* b_scales, int64_t m, int64_t n,
+                                int64_t k, int32_t out_dt, const inferop_gemm_launch* launch,
+                                void* stream);
+
+/* ---- device self-test of the E4M3 conversions used by the fast paths ----
+ * counts[0]: fp32 patterns in [lo, hi) inside the quantizer fast-path domain
+ *            (finite, |v| < 464) where the hardware encode differs from the
+ *            software (reference-semantics) encode;
+ * counts[1]: same, outside that domain (informational);
+ * counts[2]: checksum sum_i sw_encode(i) * ((i * 2654435761) mod 2^32);
+ * counts[3]: bytes 0..255 whose hardware decode differs from the software
+ *            decode (bitwise, NaNs compared as NaN).
+ * counts must point to 4 device uint64 zero-initialised by the caller. */
+int inferop_hip_selftest_fp8_codec(uint64_t lo, uint64_t hi, uint64_t* counts, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,293 @@
+// C++ front end of libinferop: the drop-in ops.h API and its C-ABI twin.
+//
+// Built with g++ and no HIP headers.  It owns what the reference keeps in
+// kernels/api.cu and the *_impl functions (argument guards, dtype switch,
+// device introspection) and the gfx950 tile selection that replaces the
+// reference's SM-version switch (kernels/gemm/w8a8_block_fp8.cu:142-159).
+// Kernels are reached through the thin C launch layer in hip_launch.h.
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+
+#include "hip_launch.h"
+#include "inferop/inferop_c.h"
+#include "inferop/ops.h"
+
+namespace inferop {
+namespace {
+
+// ---- device table (reference api.cu:12-34, made thread-safe) ---------------
+constexpr int kMaxDevices = 64;
+
+struct DeviceEntry {
+  std::once_flag once;
+  bool ok = false;
+  int arch = -1;
+  int cus = 0;
+  char name[128] = "-";
+};
+
+struct DeviceTable {
+  std::once_flag once;
+  int count = 0;
+  DeviceEntry dev[kMaxDevices];
+};
+
+DeviceTable& table() {
+  static DeviceTable t;
+  std::call_once(t.once, [] { t.count = inferop_hip_device_count(); });
+  return t;
+}
+
+const DeviceEntry* device(int ordinal) {
+  DeviceTable& t = table();
+  if (ordinal < 0 || ordinal >= t.count || ordinal >= kMaxDevices) return nullptr;
+  DeviceEntry& d = t.dev[ordinal];
+  std::call_once(d.once, [&] {
+    d.ok = inferop_hip_device_info(ordinal, d.name, sizeof(d.name), &d.arch, &d.cus) == 0;
+    if (!d.ok) std::snprintf(d.name, sizeof(d.name), "-");
+  });
+  return d.ok ? &d : nullptr;
+}
+
+const DeviceEntry* current_device() {
+  int ord = 0;
+  if (inferop_hip_current_device(&ord) != 0) return nullptr;
+  return device(ord);
+}
+
+bool valid_input_dtype(int32_t dt) { return dt == 0 || dt == 1 || dt == 2; }
+
+int status_of_hip(int e) { return e == 0 ? INFEROP_OK : INFEROP_ERR_LAUNCH; }
+
+// ---- gfx950 tile selection ----------------------------------------------------
+// Kernel table indices (inferop_amd/csrc/gemm.hip, kCfgs).
+enum GemmCfg : int32_t {
+  kN128M128 = 0,
+  kN64M16 = 1,
+  kN64M32 = 2,
+  kN64M64 = 3,
+  kN256M128 = 4,
+  kN128M256 = 5,
+};
+
+struct GemmChoice {
+  int32_t cfg;
+  int32_t split;
+};
+
+GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
+  if (cus <= 0) cus = 256;
+  const int64_t kg = k / 128;
+  int32_t cfg;
+  int64_t bn, bm;
+  if (m <= 16) {
+    cfg = kN64M16, bn = 64, bm = 16;
+  } else if (m <= 32) {
+    cfg = kN64M32, bn = 64, bm = 32;
+  } else if (m <= 64) {
+    cfg = kN64M64, bn = 64, bm = 64;
+  } else {
+    cfg = kN128M128, bn = 128, bm = 128;
+  }
+  const int64_t tiles = ((n + bn - 1) / bn) * ((m + bm - 1) / bm);
+  int64_t split = 1;
+  if (bm <= 64) {
+    // HBM-bound decode shapes: enough workgroups to keep every CU streaming
+    // weights, at least two scale groups per split.
+    const int64_t want = 2 * int64_t(cus);
+    split = (want + tiles - 1) / tiles;
+    if (split > kg / 2) split = kg / 2;
+    if (split > 16) split = 16;
+  } else if (tiles < cus) {
+    split = (cus + tiles - 1) / tiles;
+    if (split > kg / 4) split = kg / 4;
+  }
+  if (split < 1) split = 1;
+  return {cfg, int32_t(split)};
+}
+
+// ---- implementations shared by the C++ and C entry points --------------------
+int quant_impl(void* q, void* scales, const void* x, int32_t dt, int64_t rows, int64_t cols,
+               int32_t group_size, void* stream) {
+  // reference quant.cu:52 guard, then the dtype switch of quant.cu:56-74.
+  if (rows <= 0 || cols <= 0 || group_size <= 0 || cols % group_size != 0) return INFEROP_ERR_SHAPE;
+  if (!valid_input_dtype(dt)) return INFEROP_ERR_DTYPE;
+  if (!current_device()) return INFEROP_ERR_DEVICE;
+  return status_of_hip(inferop_hip_quant_fp8_group(q, static_cast<float*>(scales), x, dt, rows, cols,
+                                                   group_size, stream));
+}
+
+int dequant_impl(void* x, int32_t dt, const void* q, const void* scales, int64_t rows,
+                 int64_t cols, int32_t group_size, void* stream) {
+  // reference quant.cu:79 guard and quant.cu:84-102 dtype switch.
+  if (rows <= 0 || cols <= 0 || group_size <= 0 || cols % group_size != 0) return INFEROP_ERR_SHAPE;
+  if (!valid_input_dtype(dt)) return INFEROP_ERR_DTYPE;
+  if (!current_device()) return INFEROP_ERR_DEVICE;
+  return status_of_hip(inferop_hip_dequant_fp8_group(x, dt, static_cast<const uint8_t*>(q),
+                                                     static_cast<const float*>(scales), rows, cols,
+                                                     group_size, stream));
+}
+
+bool gemm_shape_ok(int64_t m, int64_t n, int64_t k, int32_t group_size, int32_t block_n) {
+  // reference w8a8_block_fp8.cu:167-173, including its diagnostic line.
+  if (group_size != 128 || block_n != 128 || k % 128 != 0 || m <= 0 || n <= 0) {
+    std::fprintf(stderr,
+                 "[inferop] w8a8_block_fp8_gemm: unsupported shape (m=%lld n=%lld k=%lld gs=%d "
+                 "bn=%d); v0.1 requires gs=bn=128, k%%128==0\n",
+                 (long long)m, (long long)n, (long long)k, group_size, block_n);
+    return false;
+  }
+  return true;
+}
+
+const DeviceEntry* gemm_device() {
+  const DeviceEntry* d = current_device();
+  if (!d || d->arch != 0x950) {
+    // The kernels are built for gfx950 only (arch parsed as hex digits: 0x950).
+    static std::once_flag warned;
+    std::call_once(warned, [] {
+      std::fprintf(stderr, "[inferop] w8a8_block_fp8_gemm: current device is not gfx950\n");
+    });
+    return nullptr;
+  }
+  return d;
+}
+
+int gemm_launch(void* c, const void* a_q, const void* a_scales, const void* b_q,
+                const void* b_scales, int64_t m, int64_t n, int64_t k, int32_t out_dt, int32_t cfg,
+                int32_t split, void* stream) {
+  inferop_gemm_launch l{cfg, split};
+  return status_of_hip(inferop_hip_gemm_w8a8_block(
+      c, static_cast<const uint8_t*>(a_q), static_cast<const float*>(a_scales),
+      static_cast<const uint8_t*>(b_q), static_cast<const float*>(b_scales), m, n, k, out_dt, &l,
+      stream));
+}
+
+int gemm_impl(void* c, const void* a_q, const void* a_scales, const void* b_q,
+              const void* b_scales, int64_t m, int64_t n, int64_t k, int32_t group_size,
+              int32_t block_n, int32_t out_dt, void* stream) {
+  if (!gemm_shape_ok(m, n, k, group_size, block_n)) return INFEROP_ERR_SHAPE;
+  if (!valid_input_dtype(out_dt)) return INFEROP_ERR_DTYPE;  // reference :185-186 silent no-op
+  const DeviceEntry* d = gemm_device();
+  if (!d) return INFEROP_ERR_DEVICE;
+  const GemmChoice ch = select_gemm(m, n, k, d->cus);
+  return gemm_launch(c, a_q, a_scales, b_q, b_scales, m, n, k, out_dt, ch.cfg, ch.split, stream);
+}
+
+}  // namespace
+
+// ---- ops.h --------------------------------------------------------------------
+bool has_cuda() { return table().count > 0; }
+
+int device_count() { return table().count; }
+
+const char* device_name(int ordinal) {
+  const DeviceEntry* d = device(ordinal);
+  return d ? d->name : "-";
+}
+
+int device_sm_version(int ordinal) {
+  const DeviceEntry* d = device(ordinal);
+  if (!d || d->arch < 0) return -1;
+  // arch holds the gfx digits read as hex (gfx950 -> 0x950); report them as
+  // the decimal-looking number 950 (gfx90a -> 0x90a is reported as 2314).
+  int v = d->arch;
+  if (((v >> 8) & 0xF) <= 9 && ((v >> 4) & 0xF) <= 9 && (v & 0xF) <= 9)
+    return ((v >> 8) & 0xF) * 100 + ((v >> 4) & 0xF) * 10 + (v & 0xF);
+  return v;
+}
+
+void quant_fp8_per_token_group(void* q, void* scales, const void* x, dtype dt, int64_t rows,
+                               int64_t cols, int group_size, void* stream) {
+  (void)quant_impl(q, scales, x, int32_t(dt), rows, cols, group_size, stream);
+}
+
+void dequant_fp8_per_token_group(void* x, dtype dt, const void* q, const void* scales,
+                                 int64_t rows, int64_t cols, int group_size, void* stream) {
+  (void)dequant_impl(x, int32_t(dt), q, scales, rows, cols, group_size, stream);
+}
+
+void w8a8_block_fp8_gemm(void* c, const void* a_q, const void* a_scales, const void* b_q,
+                         const void* b_scales, int64_t m, int64_t n, int64_t k, int group_size,
+                         int block_n, dtype out_dt, void* stream) {
+  (void)gemm_impl(c, a_q, a_scales, b_q, b_scales, m, n, k, group_size, block_n,
+                  int32_t(out_dt), stream);
+}
+
+}  // namespace inferop
+
+// ---- inferop_c.h ------------------------------------------------------------------
+using namespace inferop;
+
+extern "C" const char* inferop_status_string(int status) {
+  switch (status) {
+    case INFEROP_OK: return "ok";
+    case INFEROP_ERR_SHAPE: return "unsupported shape";
+    case INFEROP_ERR_DTYPE: return "unsupported dtype";
+    case INFEROP_ERR_DEVICE: return "no usable gfx950 device";
+    case INFEROP_ERR_LAUNCH: return "HIP runtime error";
+    case INFEROP_ERR_ARGUMENT: return "invalid argument";
+  }
+  return "unknown status";
+}
+
+extern "C" int inferop_has_device(void) { return has_cuda() ? 1 : 0; }
+extern "C" int inferop_device_count(void) { return device_count(); }
+extern "C" const char* inferop_device_name(int ordinal) { return device_name(ordinal); }
+extern "C" int inferop_device_arch(int ordinal) { return device_sm_version(ordinal); }
+
+extern "C" int inferop_quant_fp8_per_token_group(void* q, void* scales, const void* x, int32_t dt,
+                                                 int64_t rows, int64_t cols, int32_t group_size,
+                                                 void* stream) {
+  return quant_impl(q, scales, x, dt, rows, cols, group_size, stream);
+}
+
+extern "C" int inferop_dequant_fp8_per_token_group(void* x, int32_t dt, const void* q,
+                                                   const void* scales, int64_t rows, int64_t cols,
+                                                   int32_t group_size, void* stream) {
+  return dequant_impl(x, dt, q, scales, rows, cols, group_size, stream);
+}
+
+extern "C" int inferop_w8a8_block_fp8_gemm(void* c, const void* a_q, const void* a_scales,
+                                           const void* b_q, const void* b_scales, int64_t m,
+                                           int64_t n, int64_t k, int32_t group_size,
+                                           int32_t block_n, int32_t out_dt, void* stream) {
+  return gemm_impl(c, a_q, a_scales, b_q, b_scales, m, n, k, group_size, block_n, out_dt, stream);
+}
+
+extern "C" int inferop_gemm_num_configs(void) { return inferop_hip_gemm_num_configs(); }
+
+extern "C" const char* inferop_gemm_config_name(int config) {
+  inferop_gemm_cfg_info info;
+  if (inferop_hip_gemm_config_info(config, &info) != 0) return "invalid";
+  return info.name;
+}
+
+extern "C" int inferop_w8a8_block_fp8_gemm_config(void* c, const void* a_q, const void* a_scales,
+                                                  const void* b_q, const void* b_scales, int64_t m,
+                                                  int64_t n, int64_t k, int32_t out_dt,
+                                                  int32_t config, int32_t split_k, void* stream) {
+  if (!gemm_shape_ok(m, n, k, 128, 128)) return INFEROP_ERR_SHAPE;
+  if (!valid_input_dtype(out_dt)) return INFEROP_ERR_DTYPE;
+  if (config < 0 || config >= inferop_hip_gemm_num_configs() || split_k < 1)
+    return INFEROP_ERR_ARGUMENT;
+  if (!gemm_device()) return INFEROP_ERR_DEVICE;
+  return gemm_launch(c, a_q, a_scales, b_q, b_scales, m, n, k, out_dt, config, split_k, stream);
+}
+
+extern "C" int inferop_gemm_select(int64_t m, int64_t n, int64_t k, int32_t* config,
+                                   int32_t* split_k) {
+  if (m <= 0 || n <= 0 || k <= 0 || k % 128 != 0 || !config || !split_k) return INFEROP_ERR_ARGUMENT;
+  const DeviceEntry* d = current_device();
+  const GemmChoice ch = select_gemm(m, n, k, d ? d->cus : 256);
+  *config = ch.cfg;
+  *split_k = ch.split;
+  return INFEROP_OK;
+}
+
+extern "C" int inferop_selftest_fp8_codec(uint64_t lo, uint64_t hi, uint64_t* counts,
+                                          void* stream) {
+  if (!current_device()) return INFEROP_ERR_DEVICE;
+  return status_of_hip(inferop_hip_selftest_fp8_codec(lo, hi, counts, stream));
+}

@@ -1,0 +1,326 @@
+// Per-token-group FP8 (E4M3) quantizer and dequantizer for gfx950.
+//
+// Semantics (byte-exact with reference/reference.cpp:65-80 as compiled for
+// x86-64): per group of `group_size` consecutive elements of a row,
+//   absmax = max |x| ignoring NaN
+//   scale  = absmax == 0 ? 1 : absmax * fl32(1/448)
+//   q      = e4m3_rn_sat(x / scale), x / scale correctly rounded.
+//
+// Fast kernel (group_size == 128, 16-byte aligned input): one 128-element
+// group is one 16-lane DPP row, each lane owns 8 consecutive elements (one
+// 16-byte load for bf16/fp16, two for fp32) so a wave moves 4 whole groups
+// per load instruction, fully coalesced.  absmax is an integer max over the
+// magnitude bits (v_pk_max_u16 for 16-bit inputs) followed by a 4-step DPP
+// row reduction; no LDS, no barriers.
+//
+// The quotient: for fp32 input it is the IEEE division.  For bf16 / fp16
+// input it is r = 1/scale (IEEE, once per group) then the Markstein
+// correction q0 = x*r, e = fma(-q0, scale, x), q = fma(e, r, q0), with the
+// sign of x restored (the correction can turn -0 into +0).  The test-suite
+// checks every (x, absmax) pair of bf16 and fp16 values the fast path admits:
+// q == x/scale bit for bit wherever |x/scale| >= 2^-11, and the E4M3 byte
+// equal everywhere.  The E4M3 encode is the hardware
+// v_cvt_pk_fp8_f32, proven equal to the reference encoder on that domain by
+// inferop_selftest_fp8_codec.
+//
+// Groups containing Inf/NaN, or with 0 < absmax < 2^-80 (where the quotient
+// residual or the scale can be subnormal), take a per-group slow path with the IEEE division and
+// the software encoder, and reproduce x86-64 NaN results: a NaN element keeps
+// its sign (0x7F / 0xFF), an invalid quotient (0/0, Inf/Inf) is the negative
+// default NaN (0xFF).
+#include "device_common.h"
+#include "hip_launch.h"
+#include "quant_math.h"
+
+namespace inferop_hip {
+namespace {
+
+using inferop_qmath::kFastMinAbsmaxBits;
+using inferop_qmath::kInv448;
+
+// Per-dtype view of the 8 elements a lane owns, held as raw 32-bit words.
+template <int DT>
+struct In;
+
+template <>
+struct In<kBf16> {
+  static constexpr int kWords = 4;
+  static constexpr uint32_t kInfKey = 0x7F80u;
+  __device__ static float elem(const uint32_t* w, int i) {
+    return (i & 1) ? u2f(w[i >> 1] & 0xFFFF0000u) : u2f(w[i >> 1] << 16);
+  }
+  __device__ static float key_to_float(uint32_t key) { return u2f(key << 16); }
+  __device__ static uint32_t key(const uint32_t* w) {
+    u16x2 m = __builtin_bit_cast(u16x2, w[0] & 0x7FFF7FFFu);
+#pragma unroll
+    for (int i = 1; i < kWords; ++i)
+      m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, w[i] & 0x7FFF7FFFu));
+    return max((uint32_t)m.x, (uint32_t)m.y);
+  }
+};
+
+template <>
+struct In<kFp16> {
+  static constexpr int kWords = 4;
+  static constexpr uint32_t kInfKey = 0x7C00u;
+  __device__ static float elem(const uint32_t* w, int i) {
+    const uint16_t h = (i & 1) ? uint16_t(w[i >> 1] >> 16) : uint16_t(w[i >> 1]);
+    return (float)__builtin_bit_cast(_Float16, h);
+  }
+  __device__ static float key_to_float(uint32_t key) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)key);
+  }
+  __device__ static uint32_t key(const uint32_t* w) {
+    u16x2 m = __builtin_bit_cast(u16x2, w[0] & 0x7FFF7FFFu);
+#pragma unroll
+    for (int i = 1; i < kWords; ++i)
+      m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, w[i] & 0x7FFF7FFFu));
+    return max((uint32_t)m.x, (uint32_t)m.y);
+  }
+};
+
+template <>
+struct In<kFp32> {
+  static constexpr int kWords = 8;
+  static constexpr uint32_t kInfKey = 0x7F800000u;
+  __device__ static float elem(const uint32_t* w, int i) { return u2f(w[i]); }
+  __device__ static float key_to_float(uint32_t key) { return u2f(key); }
+  __device__ static uint32_t key(const uint32_t* w) {
+    uint32_t m = w[0] & 0x7FFFFFFFu;
+#pragma unroll
+    for (int i = 1; i < kWords; ++i) m = max(m, w[i] & 0x7FFFFFFFu);
+    return m;
+  }
+};
+
+// Magnitude bits of an fp32 value with NaN mapped to 0 (std::max semantics:
+// a NaN element never becomes the running maximum).
+__device__ __forceinline__ uint32_t mag_nonan(float v) {
+  const uint32_t a = f2u(v) & 0x7FFFFFFFu;
+  return a > 0x7F800000u ? 0u : a;
+}
+
+// Reference-exact code for any x and any scale (slow path).
+__device__ __forceinline__ uint32_t slow_code(float x, float s) {
+  if (x != x) return ((f2u(x) >> 24) & 0x80u) | 0x7Fu;
+  const float qv = x / s;
+  if (qv != qv) return 0xFFu;
+  return sw_e4m3(qv);
+}
+
+template <int DT, int U>
+__global__ __launch_bounds__(256) void quant_g128_kernel(uint8_t* __restrict__ q,
+                                                         float* __restrict__ scales,
+                                                         const uint32_t* __restrict__ x,
+                                                         int64_t ngroups) {
+  using I = In<DT>;
+  constexpr int W = I::kWords;
+  constexpr int kGroupWords = W * 16;  // 32-bit words per 128-element group
+  const int lane = threadIdx.x & 63;
+  const int sub = lane & 15;
+  const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t g0 = wave * (4 * U) + (lane >> 4);
+
+  uint32_t w[U][W];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t g = g0 + 4 * u;
+    if (g < ngroups) {
+      const u32x4* src = reinterpret_cast<const u32x4*>(x + g * kGroupWords + sub * W);
+#pragma unroll
+      for (int v = 0; v < W / 4; ++v) {
+        const u32x4 t = __builtin_nontemporal_load(src + v);
+        w[u][4 * v + 0] = t.x;
+        w[u][4 * v + 1] = t.y;
+        w[u][4 * v + 2] = t.z;
+        w[u][4 * v + 3] = t.w;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < W; ++i) w[u][i] = 0;
+    }
+  }
+
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t g = g0 + 4 * u;
+    uint32_t key = row16_max_u32(I::key(w[u]));
+    float amax = I::key_to_float(key);
+    float s = (key == 0) ? 1.0f : amax * kInv448;
+    uint32_t lo, hi;
+    const bool slow = key >= I::kInfKey || (key != 0 && f2u(amax) < kFastMinAbsmaxBits);
+    if (!slow) {
+      float v[8];
+      if constexpr (DT == kFp32) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = I::elem(w[u], i) / s;
+      } else {
+        const float r = 1.0f / s;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = inferop_qmath::div_by_recip(I::elem(w[u], i), s, r);
+      }
+      lo = cvt_pk4_e4m3(v[0], v[1], v[2], v[3]);
+      hi = cvt_pk4_e4m3(v[4], v[5], v[6], v[7]);
+    } else {
+      uint32_t k2 = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) k2 = max(k2, mag_nonan(I::elem(w[u], i)));
+      k2 = row16_max_u32(k2);
+      s = (k2 == 0) ? 1.0f : u2f(k2) * kInv448;
+      uint32_t c[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) c[i] = slow_code(I::elem(w[u], i), s);
+      lo = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+      hi = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
+    }
+    if (g < ngroups) {
+      u32x2* dst = reinterpret_cast<u32x2*>(q + g * 128 + sub * 8);
+      __builtin_nontemporal_store(u32x2{lo, hi}, dst);
+      if (sub == 0) scales[g] = s;
+    }
+  }
+}
+
+// Any group size, any alignment: one wave per group, grid-stride.
+template <int DT>
+__device__ __forceinline__ float load_elem(const void* x, int64_t i) {
+  if constexpr (DT == kFp32) {
+    return reinterpret_cast<const float*>(x)[i];
+  } else if constexpr (DT == kBf16) {
+    return u2f(uint32_t(reinterpret_cast<const uint16_t*>(x)[i]) << 16);
+  } else {
+    return (float)reinterpret_cast<const _Float16*>(x)[i];
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void quant_generic_kernel(uint8_t* __restrict__ q,
+                                                            float* __restrict__ scales,
+                                                            const void* __restrict__ x,
+                                                            int64_t ngroups, int gs) {
+  const int lane = threadIdx.x & 63;
+  const int64_t nwaves = (int64_t)gridDim.x * 4;
+  for (int64_t g = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); g < ngroups; g += nwaves) {
+    const int64_t base = g * gs;
+    uint32_t key = 0;
+    for (int i = lane; i < gs; i += 64) key = max(key, mag_nonan(load_elem<DT>(x, base + i)));
+    key = row16_max_u32(key);
+    key = max(max((uint32_t)__builtin_amdgcn_readlane((int)key, 0),
+                  (uint32_t)__builtin_amdgcn_readlane((int)key, 16)),
+              max((uint32_t)__builtin_amdgcn_readlane((int)key, 32),
+                  (uint32_t)__builtin_amdgcn_readlane((int)key, 48)));
+    const float s = (key == 0) ? 1.0f : u2f(key) * kInv448;
+    for (int i = lane; i < gs; i += 64) q[base + i] = (uint8_t)slow_code(load_elem<DT>(x, base + i), s);
+    if (lane == 0) scales[g] = s;
+  }
+}
+
+// ---- dequantizer: x = dt(e4m3_to_float(q) * scale)  (reference quant.cu:37-46)
+template <int DT>
+__global__ __launch_bounds__(256) void dequant_v16_kernel(void* __restrict__ x,
+                                                          const uint8_t* __restrict__ q,
+                                                          const float* __restrict__ scales,
+                                                          int64_t nvec, int gs) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= nvec) return;
+  const uint4 b = reinterpret_cast<const uint4*>(q)[t];
+  const float s = scales[(t * 16) / gs];
+  const uint32_t words[4] = {b.x, b.y, b.z, b.w};
+  float v[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const f32x2 lo = cvt_pk2_e4m3_f32<false>(words[i]);
+    const f32x2 hi = cvt_pk2_e4m3_f32<true>(words[i]);
+    v[4 * i + 0] = lo.x * s;
+    v[4 * i + 1] = lo.y * s;
+    v[4 * i + 2] = hi.x * s;
+    v[4 * i + 3] = hi.y * s;
+  }
+  using T = typename OutT<DT>::T;
+  T* dst = reinterpret_cast<T*>(x) + t * 16;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) store4<DT>(dst + 4 * i, v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void dequant_generic_kernel(void* __restrict__ x,
+                                                              const uint8_t* __restrict__ q,
+                                                              const float* __restrict__ scales,
+                                                              int64_t total, int gs) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const float v = inferop::fp8::e4m3_to_float(q[i]) * scales[i / gs];
+  store1<DT>(reinterpret_cast<typename OutT<DT>::T*>(x) + i, v);
+}
+
+template <int DT>
+hipError_t launch_quant(void* q, float* scales, const void* x, int64_t rows, int64_t cols, int gs,
+                        hipStream_t st) {
+  const int64_t ngroups = rows * (cols / gs);
+  const bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)q % 8 == 0) && ((uintptr_t)scales % 4 == 0);
+  if (gs == 128 && aligned) {
+    constexpr int U = 2;
+    const int64_t per_block = 16 * U;
+    const int64_t blocks = (ngroups + per_block - 1) / per_block;
+    if (blocks > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL((quant_g128_kernel<DT, U>), dim3((unsigned)blocks), dim3(256), 0, st,
+                       (uint8_t*)q, scales, (const uint32_t*)x, ngroups);
+  } else {
+    int64_t blocks = (ngroups + 3) / 4;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL((quant_generic_kernel<DT>), dim3((unsigned)blocks), dim3(256), 0, st,
+                       (uint8_t*)q, scales, x, ngroups, gs);
+  }
+  return hipGetLastError();
+}
+
+template <int DT>
+hipError_t launch_dequant(void* x, const uint8_t* q, const float* scales, int64_t rows,
+                          int64_t cols, int gs, hipStream_t st) {
+  const int64_t total = rows * cols;
+  const int ob = DT == kFp32 ? 4 : 2;
+  const bool vec = (gs % 16 == 0) && ((uintptr_t)q % 16 == 0) && ((uintptr_t)x % (4 * ob) == 0) &&
+                   total % 16 == 0;
+  if (vec) {
+    const int64_t nvec = total / 16;
+    const int64_t blocks = (nvec + 255) / 256;
+    if (blocks > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL((dequant_v16_kernel<DT>), dim3((unsigned)blocks), dim3(256), 0, st, x, q,
+                       scales, nvec, gs);
+  } else {
+    const int64_t blocks = (total + 255) / 256;
+    if (blocks > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL((dequant_generic_kernel<DT>), dim3((unsigned)blocks), dim3(256), 0, st, x, q,
+                       scales, total, gs);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+}  // namespace inferop_hip
+
+using namespace inferop_hip;
+
+extern "C" int inferop_hip_quant_fp8_group(void* q, float* scales, const void* x, int32_t dt,
+                                           int64_t rows, int64_t cols, int32_t group_size,
+                                           void* stream) {
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (dt) {
+    case kFp32: return launch_quant<kFp32>(q, scales, x, rows, cols, group_size, st);
+    case kFp16: return launch_quant<kFp16>(q, scales, x, rows, cols, group_size, st);
+    case kBf16: return launch_quant<kBf16>(q, scales, x, rows, cols, group_size, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+extern "C" int inferop_hip_dequant_fp8_group(void* x, int32_t dt, const uint8_t* q,
+                                             const float* scales, int64_t rows, int64_t cols,
+                                             int32_t group_size, void* stream) {
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (dt) {
+    case kFp32: return launch_dequant<kFp32>(x, q, scales, rows, cols, group_size, st);
+    case kFp16: return launch_dequant<kFp16>(x, q, scales, rows, cols, group_size, st);
+    case kBf16: return launch_dequant<kBf16>(x, q, scales, rows, cols, group_size, st);
+    default: return hipErrorInvalidValue;
+  }
+}

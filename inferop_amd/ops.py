@@ -1,0 +1,179 @@
+"""Python mirror of the reference's ``inferop`` operator API for the FP8 path.
+
+Same names, argument order and meaning as include/inferop/ops.h (reference
+ops.h:19-25, 64-70, 81-84): tensors are device pointers (ints) or torch
+tensors, ``dt`` / ``out_dt`` are ``dtype`` values, ``stream`` defaults to the
+current torch stream.  Like the reference, the raw calls never raise on a bad
+shape or dtype: they do nothing and return the C-ABI status code
+(``Status.OK`` when the kernels were launched).  ``quantize``, ``dequantize``
+and ``gemm`` are tensor-level conveniences that allocate outputs with torch
+and raise on any error.
+
+Every call goes to the HIP kernels in libinferop.so; there is no CPU path.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+
+from ._lib import lib
+
+
+class dtype(enum.IntEnum):
+    fp32 = 0
+    fp16 = 1
+    bf16 = 2
+    fp8_e4m3 = 3
+
+
+class Status(enum.IntEnum):
+    OK = 0
+    ERR_SHAPE = 1
+    ERR_DTYPE = 2
+    ERR_DEVICE = 3
+    ERR_LAUNCH = 4
+    ERR_ARGUMENT = 5
+
+
+class InferopError(RuntimeError):
+    def __init__(self, status: int, what: str):
+        self.status = status
+        msg = lib().inferop_status_string(int(status)).decode()
+        super().__init__(f"{what}: {msg} (status {int(status)})")
+
+
+def _ptr(t) -> int:
+    if t is None:
+        return 0
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def _stream(stream) -> int:
+    if stream is None:
+        try:
+            import torch
+            if torch.cuda.is_available():
+                return torch.cuda.current_stream().cuda_stream
+        except Exception:  # torch without a device: null stream
+            pass
+        return 0
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+# ---- ops.h:19-25 ------------------------------------------------------------
+def has_cuda() -> bool:
+    return bool(lib().inferop_has_device())
+
+
+def device_count() -> int:
+    return lib().inferop_device_count()
+
+
+def device_name(ordinal: int = 0) -> str:
+    return lib().inferop_device_name(ordinal).decode()
+
+
+def device_sm_version(ordinal: int = 0) -> int:
+    return lib().inferop_device_arch(ordinal)
+
+
+# ---- ops.h:64-65 ------------------------------------------------------------
+def quant_fp8_per_token_group(q, scales, x, dt, rows: int, cols: int, group_size: int = 128,
+                              stream=None) -> int:
+    return lib().inferop_quant_fp8_per_token_group(
+        _ptr(q), _ptr(scales), _ptr(x), int(dt), rows, cols, group_size, _stream(stream))
+
+
+# ---- ops.h:68-70 ------------------------------------------------------------
+def dequant_fp8_per_token_group(x, dt, q, scales, rows: int, cols: int, group_size: int = 128,
+                                stream=None) -> int:
+    return lib().inferop_dequant_fp8_per_token_group(
+        _ptr(x), int(dt), _ptr(q), _ptr(scales), rows, cols, group_size, _stream(stream))
+
+
+# ---- ops.h:81-84 ------------------------------------------------------------
+def w8a8_block_fp8_gemm(c, a_q, a_scales, b_q, b_scales, m: int, n: int, k: int,
+                        group_size: int = 128, block_n: int = 128, out_dt=dtype.bf16,
+                        stream=None) -> int:
+    return lib().inferop_w8a8_block_fp8_gemm(
+        _ptr(c), _ptr(a_q), _ptr(a_scales), _ptr(b_q), _ptr(b_scales), m, n, k, group_size,
+        block_n, int(out_dt), _stream(stream))
+
+
+# ---- tuning entry points (no reference counterpart) ------------------------------
+def gemm_num_configs() -> int:
+    return lib().inferop_gemm_num_configs()
+
+
+def gemm_config_name(config: int) -> str:
+    return lib().inferop_gemm_config_name(config).decode()
+
+
+def gemm_select(m: int, n: int, k: int):
+    cfg, split = ctypes.c_int32(), ctypes.c_int32()
+    st = lib().inferop_gemm_select(m, n, k, ctypes.byref(cfg), ctypes.byref(split))
+    if st != Status.OK:
+        raise InferopError(st, "gemm_select")
+    return cfg.value, split.value
+
+
+def w8a8_block_fp8_gemm_config(c, a_q, a_scales, b_q, b_scales, m: int, n: int, k: int,
+                               out_dt, config: int, split_k: int = 1, stream=None) -> int:
+    return lib().inferop_w8a8_block_fp8_gemm_config(
+        _ptr(c), _ptr(a_q), _ptr(a_scales), _ptr(b_q), _ptr(b_scales), m, n, k, int(out_dt),
+        config, split_k, _stream(stream))
+
+
+def selftest_fp8_codec(counts, lo: int = 0, hi: int = 1 << 32, stream=None) -> int:
+    return lib().inferop_selftest_fp8_codec(lo, hi, _ptr(counts), _stream(stream))
+
+
+# ---- tensor-level conveniences ---------------------------------------------------
+def _torch_dtype_code(t) -> dtype:
+    import torch
+    return {torch.float32: dtype.fp32, torch.float16: dtype.fp16,
+            torch.bfloat16: dtype.bf16}[t]
+
+
+def quantize(x, group_size: int = 128, stream=None):
+    """x: [rows, cols] fp32/fp16/bf16 device tensor -> (q uint8, scales fp32)."""
+    import torch
+    rows, cols = x.shape
+    x = x.contiguous()
+    q = torch.empty((rows, cols), dtype=torch.uint8, device=x.device)
+    s = torch.empty((rows, cols // group_size), dtype=torch.float32, device=x.device)
+    st = quant_fp8_per_token_group(q, s, x, _torch_dtype_code(x.dtype), rows, cols, group_size,
+                                   stream)
+    if st != Status.OK:
+        raise InferopError(st, "quant_fp8_per_token_group")
+    return q, s
+
+
+def dequantize(q, scales, out_dtype=None, group_size: int = 128, stream=None):
+    import torch
+    out_dtype = out_dtype or torch.bfloat16
+    rows, cols = q.shape
+    x = torch.empty((rows, cols), dtype=out_dtype, device=q.device)
+    st = dequant_fp8_per_token_group(x, _torch_dtype_code(out_dtype), q, scales, rows, cols,
+                                     group_size, stream)
+    if st != Status.OK:
+        raise InferopError(st, "dequant_fp8_per_token_group")
+    return x
+
+
+def gemm(a_q, a_s, b_q, b_s, out_dtype=None, stream=None):
+    """C[M,N] = blockwise-FP8 product of a_q [M,K] and b_q [N,K]."""
+    import torch
+    out_dtype = out_dtype or torch.bfloat16
+    m, k = a_q.shape
+    n = b_q.shape[0]
+    c = torch.empty((m, n), dtype=out_dtype, device=a_q.device)
+    st = w8a8_block_fp8_gemm(c, a_q, a_s, b_q, b_s, m, n, k, 128, 128,
+                             _torch_dtype_code(out_dtype), stream)
+    if st != Status.OK:
+        raise InferopError(st, "w8a8_block_fp8_gemm")
+    return c

@@ -1,0 +1,186 @@
+"""GPU blockwise-FP8 GEMM parity with the oracle (reference.cpp:93-110, fp64
+accumulation) on all five BASELINE.json configs, to the stated tolerance
+max|err| <= 1e-2 * rms(C_ref) + 1 bf16 ulp."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import datagen
+import inferop_amd
+import oracle
+from gpu_util import assert_gemm_close, bf16_dev, device, out_to_f32, to_dev, to_np
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+DT = inferop_amd.dtype
+TORCH_OUT = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}
+
+
+def _gemm(aq, as_, bq, bs, m, n, k, out="bf16", config=None, split=1):
+    c = torch.full((m, n), float("nan"), dtype=TORCH_OUT[out], device="cuda:0")
+    if config is None:
+        st = inferop_amd.w8a8_block_fp8_gemm(c, aq, as_, bq, bs, m, n, k, 128, 128,
+                                             getattr(DT, out))
+    else:
+        st = inferop_amd.w8a8_block_fp8_gemm_config(c, aq, as_, bq, bs, m, n, k,
+                                                    getattr(DT, out), config, split)
+    assert st == 0
+    return c
+
+
+def _host_case(m, n, k, seed, dist="normal"):
+    a_bits, a_f32, bq, bs = datagen.gemm_case(m, n, k, seed, dist)
+    aq, as_ = oracle.quant(a_f32)
+    return a_bits, aq, as_, bq, bs
+
+
+@pytest.mark.gpu
+def test_config0_golden_end_to_end():
+    # BASELINE config 0, expected output written by the reference's own code:
+    # GPU quantizer on the bf16 activations, then the GPU GEMM
+    device()
+    g = np.load(os.path.join(GOLDEN, "config0.npz"))
+    m, k = g["a_q"].shape
+    n = g["b_q"].shape[0]
+    a = bf16_dev(g["a_bits"])
+    q, s = inferop_amd.quantize(a)
+    assert np.array_equal(to_np(q), g["a_q"])
+    assert np.array_equal(to_np(s).view(np.uint32), g["a_s"].view(np.uint32))
+    c = _gemm(q, s, to_dev(g["b_q"]), to_dev(g["b_s"]), m, n, k)
+    assert_gemm_close(out_to_f32(c), g["c_ref"], "config0")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m", [1, 16, 64])
+@pytest.mark.parametrize("nk", [(7168, 2048), (4096, 7168), (2112, 7168)])
+def test_config1_decode_full_parity(m, nk):
+    device()
+    n, k = nk
+    print(f"config1 m={m} n={n} k={k}", flush=True)
+    _, aq, as_, bq, bs = _host_case(m, n, k, seed=100 + m)
+    c = _gemm(to_dev(aq), to_dev(as_), to_dev(bq), to_dev(bs), m, n, k)
+    assert_gemm_close(out_to_f32(c), oracle.gemm(aq, as_, bq, bs), f"config1 {m}x{n}x{k}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m", [77, 1000])
+def test_config4_ragged_stress(m):
+    device()
+    n, k = 4608 + 64, 7168
+    print(f"config4 m={m}", flush=True)
+    a_bits, a_f32, bq, bs = datagen.gemm_case(m, n, k, seed=400 + m, dist="stress")
+    # quantize on the GPU; bytes must equal the oracle's
+    q, s = inferop_amd.quantize(bf16_dev(a_bits))
+    aq, as_ = oracle.quant(a_f32)
+    assert np.array_equal(to_np(q), aq)
+    c = out_to_f32(_gemm(q, s, to_dev(bq), to_dev(bs), m, n, k))
+    rows = np.arange(m) if m <= 128 else np.unique(np.concatenate(
+        [[0, m - 1, m - 2], np.random.default_rng(m).integers(0, m, 29)]))
+    want = oracle.gemm_rows(aq, as_, bq, bs, rows)
+    assert_gemm_close(c[rows], want, f"config4 m={m}")
+
+
+def _device_case(m, n, k, seed):
+    """Large shapes: inputs generated on the GPU; A quantized by the GPU
+    quantizer; weights block-quantized with torch (input preparation only --
+    the oracle receives the very same bytes)."""
+    g = torch.Generator(device="cuda:0").manual_seed(seed)
+    a = torch.randn((m, k), generator=g, device="cuda:0").to(torch.bfloat16)
+    w = torch.randn((n, k), generator=g, device="cuda:0") * 0.02
+    nb = (n + 127) // 128
+    wp = torch.zeros((nb * 128, k), device="cuda:0")
+    wp[:n] = w
+    blk = wp.view(nb, 128, k // 128, 128).abs().amax(dim=(1, 3))
+    inv448 = torch.tensor(1.0 / 448.0, dtype=torch.float32, device="cuda:0")
+    bs = torch.where(blk == 0, torch.ones_like(blk), blk * inv448)
+    inv = (1.0 / bs).repeat_interleave(128, 0).repeat_interleave(128, 1)[:n]
+    bq = (w * inv).to(torch.float8_e4m3fn).view(torch.uint8)
+    aq, as_ = inferop_amd.quantize(a)
+    return a, aq, as_, bq.contiguous(), bs.contiguous()
+
+
+def _check_sampled(a, aq, as_, bq, bs, c, rows, what):
+    aq_h, as_h = to_np(aq[rows]), to_np(as_[rows])
+    # the GPU quantizer's rows equal the oracle's on the same bf16 inputs
+    qr, sr = oracle.quant(datagen.bf16_bits_to_f32(to_np(a[rows])))
+    assert np.array_equal(aq_h, qr), what
+    assert np.array_equal(as_h.view(np.uint32), sr.view(np.uint32)), what
+    want = oracle.gemm_rows(aq_h, as_h, to_np(bq), to_np(bs), np.arange(len(rows)))
+    return assert_gemm_close(out_to_f32(c[rows]), want, what)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("nk", [(24576, 1536), (32768, 512), (7168, 16384), (4608, 7168)])
+def test_config2_prefill_sampled(nk):
+    device()
+    m = 4096
+    n, k = nk
+    print(f"config2 n={n} k={k}", flush=True)
+    a, aq, as_, bq, bs = _device_case(m, n, k, seed=200)
+    c = _gemm(aq, as_, bq, bs, m, n, k)
+    rows = np.unique(np.concatenate([[0, 1, 4095], np.random.default_rng(n).integers(0, m, 9)]))
+    _check_sampled(a, aq, as_, bq, bs, c, rows, f"config2 {n}x{k}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m", [128, 512, 1024, 2048, 8192])
+@pytest.mark.parametrize("nk", [(7168, 18432), (36864, 7168), (7168, 2048), (4096, 512)])
+def test_config3_m_sweep_sampled(m, nk):
+    device()
+    n, k = nk
+    print(f"config3 m={m} n={n} k={k}", flush=True)
+    a, aq, as_, bq, bs = _device_case(m, n, k, seed=300 + m)
+    rows = np.unique(np.concatenate([[0, m - 1], np.random.default_rng(m + n).integers(0, m, 4)]))
+    for out in ("bf16", "fp16"):
+        c = _gemm(aq, as_, bq, bs, m, n, k, out=out)
+        _check_sampled(a, aq, as_, bq, bs, c, rows, f"config3 {m}x{n}x{k} {out}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("config", range(6))
+@pytest.mark.parametrize("split", [1, 3])
+def test_every_kernel_config_ragged(config, split):
+    device()
+    m, n, k = 77, 300, 768
+    _, aq, as_, bq, bs = _host_case(m, n, k, seed=7, dist="stress")
+    want = oracle.gemm(aq, as_, bq, bs)
+    for out in ("bf16", "fp32"):
+        c = _gemm(to_dev(aq), to_dev(as_), to_dev(bq), to_dev(bs), m, n, k, out, config, split)
+        assert_gemm_close(out_to_f32(c), want, f"cfg{config} split{split} {out}")
+
+
+@pytest.mark.gpu
+def test_output_dtypes_and_odd_n():
+    device()
+    for (m, n, k) in [(40, 130, 256), (5, 7, 128), (129, 1, 384)]:
+        _, aq, as_, bq, bs = _host_case(m, n, k, seed=m + n)
+        want = oracle.gemm(aq, as_, bq, bs)
+        for out in ("bf16", "fp16", "fp32"):
+            c = _gemm(to_dev(aq), to_dev(as_), to_dev(bq), to_dev(bs), m, n, k, out)
+            assert_gemm_close(out_to_f32(c), want, f"{m}x{n}x{k} {out}")
+
+
+@pytest.mark.gpu
+def test_split_k_deterministic_and_repeatable():
+    device()
+    m, n, k = 16, 4096, 7168
+    _, aq, as_, bq, bs = _host_case(m, n, k, seed=9)
+    args = [to_dev(v) for v in (aq, as_, bq, bs)]
+    first = to_np(_gemm(*args, m, n, k))
+    for _ in range(3):
+        assert np.array_equal(to_np(_gemm(*args, m, n, k)), first)
+
+
+@pytest.mark.gpu
+def test_gemm_rejected_calls_leave_output_untouched(capfd):
+    device()
+    c = torch.full((4, 8), 5.0, dtype=torch.float32, device="cuda:0")
+    z = torch.zeros(1024, dtype=torch.uint8, device="cuda:0")
+    S = inferop_amd.Status
+    assert inferop_amd.w8a8_block_fp8_gemm(c, z, z, z, z, 4, 8, 100, out_dt=DT.fp32) == S.ERR_SHAPE
+    assert inferop_amd.w8a8_block_fp8_gemm(c, z, z, z, z, 4, 8, 128,
+                                           out_dt=DT.fp8_e4m3) == S.ERR_DTYPE
+    torch.cuda.synchronize()
+    assert (c == 5.0).all()
+    assert "unsupported shape (m=4 n=8 k=100" in capfd.readouterr().err

@@ -1,0 +1,151 @@
+"""GPU quantizer / dequantizer parity with the oracle: bytes and scales
+bit-exact (reference/reference.cpp:65-91 semantics on identical inputs)."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import datagen
+import inferop_amd
+import oracle
+from gpu_util import bf16_dev, device, f16_dev, to_dev, to_np
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+DT = inferop_amd.dtype
+
+
+def _pack(x32: np.ndarray, kind: str):
+    """(device tensor, exact fp32 values the oracle must see)."""
+    if kind == "bf16":
+        bits = datagen.f32_to_bf16_bits(x32)
+        return bf16_dev(bits), datagen.bf16_bits_to_f32(bits)
+    if kind == "fp16":
+        bits = datagen.f32_to_f16_bits(x32)
+        return f16_dev(bits), datagen.f16_bits_to_f32(bits)
+    return to_dev(x32.astype(np.float32)), x32.astype(np.float32)
+
+
+def _gpu_quant(xd, kind, rows, cols, gs=128):
+    q = torch.full((rows, cols), 0xA5, dtype=torch.uint8, device="cuda:0")
+    s = torch.full((rows, cols // gs), -7.0, dtype=torch.float32, device="cuda:0")
+    st = inferop_amd.quant_fp8_per_token_group(q, s, xd, getattr(DT, kind), rows, cols, gs)
+    assert st == 0
+    return to_np(q), to_np(s)
+
+
+def _assert_same(q, s, qr, sr, what):
+    if not np.array_equal(q, qr):
+        i = np.argwhere(q != qr)[0]
+        raise AssertionError(f"{what}: {int((q != qr).sum())} byte mismatches, first at {i}: "
+                             f"got {q[tuple(i)]:#x} want {qr[tuple(i)]:#x}")
+    assert np.array_equal(s.view(np.uint32), sr.view(np.uint32)), what
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind", ["bf16", "fp16", "fp32"])
+@pytest.mark.parametrize("shape,dist", [((16, 1024), "normal"), ((1, 2048), "normal"),
+                                        ((64, 7168), "normal"), ((77, 7168), "stress"),
+                                        ((1000, 7168), "stress"), ((3, 128), "normal")])
+def test_quant_parity(kind, shape, dist):
+    device()
+    m, k = shape
+    print(f"quant parity {kind} {shape} {dist}", flush=True)
+    xd, x32 = _pack(datagen.activations(m, k, 21, dist), kind)
+    q, s = _gpu_quant(xd, kind, m, k)
+    qr, sr = oracle.quant(x32)
+    _assert_same(q, s, qr, sr, f"{kind} {shape}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind", ["bf16", "fp16", "fp32"])
+def test_quant_edge_groups_vs_reference_fixture(kind):
+    # NaN / Inf / -0 / zero / subnormal / tiny / huge groups; expected bytes
+    # written by the reference's own compiled code
+    device()
+    g = np.load(os.path.join(GOLDEN, "quant_edges.npz"))
+    x = g[f"{kind}_x"]
+    xd, _ = _pack(x, kind)
+    q, s = _gpu_quant(xd, kind, x.shape[0], x.shape[1])
+    _assert_same(q, s, g[f"{kind}_q"], g[f"{kind}_s"], f"edges {kind}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind", ["bf16", "fp32"])
+@pytest.mark.parametrize("gs", [32, 64, 256, 96])
+def test_quant_other_group_sizes(kind, gs):
+    device()
+    m, k = 9, gs * 6
+    xd, x32 = _pack(datagen.activations(m, k, 5, "stress"), kind)
+    q, s = _gpu_quant(xd, kind, m, k, gs)
+    qr, sr = oracle.quant(x32, gs)
+    _assert_same(q, s, qr, sr, f"gs={gs}")
+
+
+@pytest.mark.gpu
+def test_quant_unaligned_input_uses_generic_path():
+    device()
+    m, k = 4, 512
+    x32 = datagen.activations(m, k + 1, 8).astype(np.float32)
+    bits = datagen.f32_to_bf16_bits(x32).reshape(-1)
+    buf = bf16_dev(bits)
+    xd = buf[1:1 + m * k]  # 2-byte offset: not 16-byte aligned
+    q, s = _gpu_quant(xd, "bf16", m, k)
+    qr, sr = oracle.quant(datagen.bf16_bits_to_f32(bits[1:1 + m * k]).reshape(m, k))
+    _assert_same(q, s, qr, sr, "unaligned")
+
+
+@pytest.mark.gpu
+def test_quant_rejected_shapes_leave_outputs_untouched():
+    device()
+    x = torch.zeros((4, 200), dtype=torch.bfloat16, device="cuda:0")
+    q = torch.full((4, 200), 0x5A, dtype=torch.uint8, device="cuda:0")
+    s = torch.full((4, 2), 3.0, dtype=torch.float32, device="cuda:0")
+    S = inferop_amd.Status
+    assert inferop_amd.quant_fp8_per_token_group(q, s, x, DT.bf16, 4, 200, 128) == S.ERR_SHAPE
+    assert inferop_amd.quant_fp8_per_token_group(q, s, x, DT.fp8_e4m3, 4, 128, 128) == S.ERR_DTYPE
+    torch.cuda.synchronize()
+    assert (q == 0x5A).all() and (s == 3.0).all()
+
+
+@pytest.mark.gpu
+def test_quant_large_sampled_rows_and_roundtrip():
+    # M=4096, K=16384 (config 2's largest K): rows sampled against the oracle,
+    # the whole tensor checked by a size-independent round-trip bound
+    device()
+    m, k = 4096, 16384
+    g = torch.Generator(device="cuda:0").manual_seed(3)
+    x = torch.randn((m, k), generator=g, device="cuda:0").to(torch.bfloat16)
+    q = torch.empty((m, k), dtype=torch.uint8, device="cuda:0")
+    s = torch.empty((m, k // 128), dtype=torch.float32, device="cuda:0")
+    assert inferop_amd.quant_fp8_per_token_group(q, s, x, DT.bf16, m, k) == 0
+    rows = np.array([0, 1, 2047, 4095] + list(np.random.default_rng(1).integers(0, m, 12)))
+    xs = to_np(x[rows]).view(np.uint16)
+    qr, sr = oracle.quant(datagen.bf16_bits_to_f32(xs))
+    _assert_same(to_np(q[rows]), to_np(s[rows]), qr, sr, "4096x16384 sampled rows")
+    # dequantize on the GPU and bound the error everywhere
+    xd = torch.empty((m, k), dtype=torch.float32, device="cuda:0")
+    assert inferop_amd.dequant_fp8_per_token_group(xd, DT.fp32, q, s, m, k) == 0
+    xf = x.float()
+    sg = s.repeat_interleave(128, dim=1)
+    tol = torch.maximum(xf.abs() / 16, sg * 1.5e-3)
+    assert bool(((xd - xf).abs() <= tol).all())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("out", ["fp32", "bf16", "fp16"])
+@pytest.mark.parametrize("gs", [128, 64, 48, 40])
+def test_dequant_parity(out, gs):
+    device()
+    m, k = 37, gs * 8
+    x32 = datagen.activations(m, k, 12, "stress")
+    qr, sr = oracle.quant(x32, gs)
+    want = oracle.dequant(qr, sr, gs)
+    xd = torch.empty((m, k), dtype={"fp32": torch.float32, "bf16": torch.bfloat16,
+                                    "fp16": torch.float16}[out], device="cuda:0")
+    assert inferop_amd.dequant_fp8_per_token_group(xd, getattr(DT, out), to_dev(qr), to_dev(sr),
+                                                   m, k, gs) == 0
+    got = xd.float().cpu().numpy()
+    # fp32: bit-exact; 16-bit: the oracle's fp32 value rounded to nearest-even
+    want_t = torch.from_numpy(want).to(xd.dtype).float().numpy()
+    assert np.array_equal(got.view(np.uint32), want_t.view(np.uint32))

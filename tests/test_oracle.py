@@ -1,0 +1,239 @@
+"""The CPU oracle pinned against the compiled reference, an independent
+encoder, closed forms and the reference tests' own known answers."""
+import math
+
+import numpy as np
+import pytest
+
+import datagen
+import oracle
+
+needs_ref = pytest.mark.skipif(not oracle.ref_available(),
+                               reason="oracle/_ref not built (reference sources absent)")
+
+
+def _grid_value(b: int) -> float:
+    """OCP E4M3FN closed form (tests/test_fp8.cpp:8-24 describes the same)."""
+    sign = -1.0 if b & 0x80 else 1.0
+    e, m = (b >> 3) & 0xF, b & 7
+    if e == 15 and m == 7:
+        return math.nan
+    if e == 0:
+        return sign * m * 2.0 ** -9
+    return sign * (1 + m / 8) * 2.0 ** (e - 7)
+
+
+def test_decode_all_bytes_closed_form():
+    L = oracle.lib()
+    for b in range(256):
+        want = _grid_value(b)
+        got = L.orc_e4m3_to_float(b)
+        if math.isnan(want):
+            assert math.isnan(got)
+        else:
+            assert got == want and math.copysign(1, got) == (-1 if b & 0x80 else 1)
+
+
+def test_encode_reference_edge_list():
+    # tests/test_fp8.cpp:75-80 edge magnitudes, both signs, against the
+    # independent grid encoder
+    L = oracle.lib()
+    for v in [0.0, 1.0, 448.0, 449.0, 464.0, 479.99998, 480.0, 512.0, 1e6, 5.9604645e-8,
+              2.9802322e-8, 1.5258789e-05, 0.0146484375, 0.015624999, 0.015625, 0.0001, 1e-9, 1e38]:
+        for s in (v, -v):
+            assert L.orc_float_to_e4m3(s) == L.orc_grid_encode(s), s
+
+
+def test_encode_grid_points_and_ties():
+    # every grid point and every midpoint (tests/test_fp8.cpp:82-91)
+    L = oracle.lib()
+    for b in range(1, 0x7E):
+        v, nxt = _grid_value(b), _grid_value(b + 1)
+        assert L.orc_float_to_e4m3(v) == b
+        mid = (v + nxt) / 2
+        want = b if b % 2 == 0 else b + 1  # tie goes to the even encoding
+        assert L.orc_float_to_e4m3(mid) == want, (b, mid)
+    assert L.orc_float_to_e4m3(464.0) == 0x7E and L.orc_float_to_e4m3(-464.0) == 0xFE
+    assert L.orc_float_to_e4m3(float("inf")) == 0x7E
+    assert L.orc_float_to_e4m3(float("nan")) & 0x7F == 0x7F
+
+
+@pytest.mark.slow
+def test_encode_exhaustive_vs_independent_grid():
+    assert oracle.lib().orc_sweep_encode_vs_grid(0, 1 << 32) == 0
+
+
+@pytest.mark.slow
+@needs_ref
+def test_encode_exhaustive_vs_reference():
+    L, R = oracle.lib(), oracle.ref()
+    chunk = 1 << 27
+    a = np.empty(chunk, np.uint8)
+    b = np.empty(chunk, np.uint8)
+    for lo in range(0, 1 << 32, chunk):
+        L.orc_encode_range(lo, lo + chunk, oracle._ptr(a, oracle._u8p))
+        R.ref_encode_range(lo, lo + chunk, oracle._ptr(b, oracle._u8p))
+        assert np.array_equal(a, b), hex(lo)
+
+
+@pytest.mark.slow
+@needs_ref
+@pytest.mark.parametrize("kind", ["bf16", "half"])
+def test_16bit_conversions_exhaustive_vs_reference(kind):
+    L, R = oracle.lib(), oracle.ref()
+    fo = getattr(L, f"orc_{kind}_range")
+    fr = getattr(R, f"ref_{kind}_range")
+    chunk = 1 << 27
+    a = np.empty(chunk, np.uint16)
+    b = np.empty(chunk, np.uint16)
+    for lo in range(0, 1 << 32, chunk):
+        fo(lo, lo + chunk, oracle._ptr(a, oracle._u16p))
+        fr(lo, lo + chunk, oracle._ptr(b, oracle._u16p))
+        assert np.array_equal(a, b), hex(lo)
+
+
+def test_half_to_float_all_vs_numpy():
+    L = oracle.lib()
+    h = np.arange(65536, dtype=np.uint32)
+    want = h.astype(np.uint16).view(np.float16).astype(np.float32)
+    got = np.array([L.orc_half_to_float(int(v)) for v in h], np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_float_to_half_matches_ieee_outside_documented_departures():
+    # common.h:80-101 is IEEE RNE except (65504, 65520) -> Inf and (2^-25, 2^-24) -> 0
+    L = oracle.lib()
+    g = np.random.default_rng(5)
+    x = np.concatenate([g.standard_normal(20000).astype(np.float32) * s
+                        for s in (1e-6, 1e-3, 1.0, 1e3, 3e4)])
+    for v in x:
+        a = abs(float(v))
+        if 65504 < a < 65520 or 2.0 ** -25 < a < 2.0 ** -24:
+            continue
+        with np.errstate(over="ignore"):
+            want = int(np.float16(v).view(np.uint16))
+        assert L.orc_float_to_half(float(v)) == want, v
+
+
+@needs_ref
+@pytest.mark.parametrize("dist", ["normal", "stress"])
+@pytest.mark.parametrize("shape", [(16, 1024), (64, 768), (77, 7168)])
+def test_quant_matches_reference(shape, dist):
+    m, k = shape
+    x = datagen.bf16_bits_to_f32(datagen.f32_to_bf16_bits(datagen.activations(m, k, 7, dist)))
+    q, s = oracle.quant(x)
+    qr, sr = oracle.ref_quant(x)
+    assert np.array_equal(q, qr)
+    assert np.array_equal(s.view(np.uint32), sr.view(np.uint32))
+
+
+@needs_ref
+@pytest.mark.parametrize("kind", ["bf16", "fp16", "fp32"])
+def test_quant_edge_groups_match_reference(kind):
+    x = datagen.special_groups(kind)
+    q, s = oracle.quant(x)
+    qr, sr = oracle.ref_quant(x)
+    assert np.array_equal(q, qr)
+    assert np.array_equal(s.view(np.uint32), sr.view(np.uint32))
+
+
+def test_quant_zero_group_known_answer():
+    # tests/test_quant.cpp:34-41: zero group -> scale exactly 1, all bytes 0
+    q, s = oracle.quant(np.zeros((1, 768), np.float32))
+    assert (s == 1.0).all() and (q == 0).all()
+
+
+def test_quant_scale_closed_form_and_roundtrip_bound():
+    # scale = absmax * fl32(1/448); round trip within the E4M3 grid bound
+    # (tests/test_quant.cpp:23-32)
+    x = datagen.activations(64, 768, 11)
+    q, s = oracle.quant(x)
+    amax = np.abs(x.reshape(64, 6, 128)).max(-1)
+    inv448 = np.float32(1.0) / np.float32(448.0)
+    assert np.float32(inv448).view(np.uint32) == 0x3B124925
+    assert np.array_equal(s, (amax * inv448).astype(np.float32))
+    dq = oracle.dequant(q, s)
+    sg = np.repeat(s, 128, axis=1)
+    tol = np.maximum(np.abs(x) / 16, sg * 1.5e-3) + 1e-30
+    assert (np.abs(dq - x) <= tol).all()
+    # the group maximum always lands on +-448
+    idx = np.abs(x.reshape(64, 6, 128)).argmax(-1)
+    qg = q.reshape(64, 6, 128)
+    assert (np.take_along_axis(qg, idx[..., None], -1) & 0x7F == 0x7E).all()
+
+
+def _dequant_f64(q, s, n_block=False):
+    table = oracle.e4m3_decode_table().astype(np.float64)
+    v = table[q]
+    if n_block:
+        sb = np.repeat(np.repeat(s, 128, axis=0)[:q.shape[0]], 128, axis=1)
+    else:
+        sb = np.repeat(s, 128, axis=1)
+    return v * sb.astype(np.float64)
+
+
+@needs_ref
+def test_gemm_bit_exact_vs_reference():
+    a_bits, a_f32, bq, bs = datagen.gemm_case(33, 300, 512, seed=3)
+    aq, as_ = oracle.quant(a_f32)
+    c = oracle.gemm(aq, as_, bq, bs)
+    cr = oracle.ref_gemm(aq, as_, bq, bs)
+    assert np.array_equal(c.view(np.uint32), cr.view(np.uint32))
+    rows = np.array([0, 5, 32])
+    assert np.array_equal(oracle.gemm_rows(aq, as_, bq, bs, rows), c[rows])
+
+
+def test_gemm_vs_float64_matmul_of_dequantized_operands():
+    a_bits, a_f32, bq, bs = datagen.gemm_case(20, 260, 384, seed=4)
+    aq, as_ = oracle.quant(a_f32)
+    c = oracle.gemm(aq, as_, bq, bs)
+    # products of fp32-rounded dequantized values, summed in fp64: the oracle's
+    # own definition; here computed by numpy's matmul
+    da = (oracle.e4m3_decode_table()[aq] * np.repeat(as_, 128, axis=1)).astype(np.float64)
+    sb = np.repeat(np.repeat(bs, 128, axis=0)[:260], 128, axis=1)
+    db = (oracle.e4m3_decode_table()[bq] * sb).astype(np.float64)
+    want = da @ db.T
+    assert np.allclose(c, want, rtol=1e-6, atol=1e-6 * np.abs(want).max())
+
+
+def test_gemm_linear_in_scales_and_k_permutation_invariant():
+    a_bits, a_f32, bq, bs = datagen.gemm_case(8, 130, 256, seed=6)
+    aq, as_ = oracle.quant(a_f32)
+    c = oracle.gemm(aq, as_, bq, bs).astype(np.float64)
+    # doubling every activation scale doubles C exactly (power-of-two scaling)
+    c2 = oracle.gemm(aq, as_ * 2, bq, bs).astype(np.float64)
+    assert np.array_equal(c2, 2 * c)
+    # zeroing the scales of group 1 removes exactly that group's contribution
+    as0 = as_.copy()
+    as0[:, 1] = 0
+    c_g0 = oracle.gemm(aq, as0, bq, bs).astype(np.float64)
+    as1 = as_.copy()
+    as1[:, 0] = 0
+    c_g1 = oracle.gemm(aq, as1, bq, bs).astype(np.float64)
+    # each side is one fp64 sum rounded once to fp32 (<= 2^-24 relative)
+    bound = 2.0 ** -23 * (np.abs(c_g0) + np.abs(c_g1) + np.abs(c))
+    assert (np.abs(c_g0 + c_g1 - c) <= bound).all()
+    # permuting K inside a group (same permutation on A and B) leaves C unchanged
+    perm = np.random.default_rng(0).permutation(128)
+    cols = np.concatenate([perm, 128 + np.arange(128)])
+    cp = oracle.gemm(aq[:, cols], as_, bq[:, cols], bs).astype(np.float64)
+    assert np.allclose(cp, c, rtol=0, atol=1e-6 * np.abs(c).max())
+
+
+def test_weight_block_quant_properties():
+    w = datagen.weights(200, 256, 9, "stress")
+    bq, bs = oracle.weight_block_quant(w)
+    assert bs.shape == (2, 2)
+    for nb in range(2):
+        for g in range(2):
+            blk = w[nb * 128:(nb + 1) * 128, g * 128:(g + 1) * 128]
+            amax = np.abs(blk).max()
+            assert bs[nb, g] == np.float32(amax * (np.float32(1) / np.float32(448)))
+            qb = bq[nb * 128:(nb + 1) * 128, g * 128:(g + 1) * 128]
+            # the block maximum encodes to +-448
+            i = np.unravel_index(np.abs(blk).argmax(), blk.shape)
+            assert qb[i] & 0x7F == 0x7E
+            deq = oracle.e4m3_decode_table()[qb] * bs[nb, g]
+            assert (np.abs(deq - blk) <= np.maximum(np.abs(blk) / 16, bs[nb, g] * 1.5e-3) + 1e-30).all()
