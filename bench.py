@@ -3,15 +3,18 @@
 Headline workload (decode-shaped): one step runs,
 for each M in {1, 16, 64} and (N, K) in {(7168, 2048), (4096, 7168),
 (2112, 7168)}, the quantizer on bf16 activations [M, K] followed by the
-blockwise-FP8 GEMM into bf16 [M, N].  `value` is the step's algorithmic HBM
-bytes divided by its wall time (GB/s), inputs resident in HBM, weights rotated
-over more than 1 GB of copies so the 256 MB Infinity Cache cannot serve them.
+blockwise-FP8 GEMM into bf16 [M, N] -- 18 kernel launches.  The step is
+captured once into a HIP graph per weight copy and replayed, the way a
+serving loop runs decode; weights rotate over more than 1 GiB of copies so
+the 256 MB Infinity Cache cannot serve them.  `value` is the step's
+algorithmic HBM bytes divided by its wall time (GB/s).
 
 Also reported: the prefill GEMM (configs[2], M = 4096) in TFLOPS against the
-5.0 PFLOPS dense-FP8 peak, the quantizer on large inputs in GB/s, per-kernel
-average durations (HIP events on the launch stream), and a CPU baseline: the
-reference's own CPU golden code (or the oracle restatement) timed on this
-host's cores over the same decode workload.
+5.0 PFLOPS dense-FP8 peak, the quantizer on large inputs in GB/s, and a CPU
+baseline (the reference's own CPU golden code, or the oracle restatement,
+timed single-threaded on this host over the same decode workload).
+Per-kernel durations come from HIP events on the launch stream around graph
+replays of back-to-back launches of one kernel.
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 """
@@ -33,6 +36,7 @@ DECODE_M = (1, 16, 64)
 DECODE_NK = ((7168, 2048), (4096, 7168), (2112, 7168))
 PREFILL_NK = ((24576, 1536), (32768, 512), (7168, 16384), (4608, 7168))
 QUANT_SHAPES = ((4096, 7168), (4096, 16384), (8192, 18432))
+PER_KERNEL_LAUNCHES = 20
 
 
 def quant_bytes(m, k, in_bytes=2):
@@ -40,57 +44,26 @@ def quant_bytes(m, k, in_bytes=2):
 
 
 def gemm_bytes(m, n, k, out_bytes=2):
-    return m * k + 4 * m * (k // 128) + n * k + 4 * ((n + 127) // 128) * (k // 128) + m * n * out_bytes
+    return (m * k + 4 * m * (k // 128) + n * k + 4 * ((n + 127) // 128) * (k // 128)
+            + m * n * out_bytes)
 
 
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=50)
-    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    p.add_argument("--only", default="", help="decode|prefill|quant (debug: one section)")
     return p.parse_args()
-
-
-class Timer:
-    """HIP events recorded on the stream the kernels are launched on."""
-
-    def __init__(self, torch, stream):
-        self.torch, self.stream = torch, stream
-
-    def span(self, fn, reps):
-        t = self.torch
-        e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
-        e0.record(self.stream)
-        for i in range(reps):
-            fn(i)
-        e1.record(self.stream)
-        e1.synchronize()
-        return e0.elapsed_time(e1) / reps  # ms per call
-
-    def each(self, fn, reps):
-        """Average duration of one launch, each bracketed by its own events."""
-        t = self.torch
-        evs = [(t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True))
-               for _ in range(reps)]
-        for i, (a, b) in enumerate(evs):
-            a.record(self.stream)
-            fn(i)
-            b.record(self.stream)
-        evs[-1][1].synchronize()
-        ds = sorted(a.elapsed_time(b) for a, b in evs)
-        return ds[len(ds) // 2], sum(ds) / len(ds)  # median, mean (ms)
 
 
 def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this benchmark runs on exactly one GPU: the FP8 path has no "
-                                   "multi-GPU component here (sharding is described in DESIGN.md); "
-                                   "run with --gpus 1"}))
+                                   "multi-GPU component here (sharding is described in "
+                                   "DESIGN.md); run with --gpus 1"}))
         sys.exit(2)
-    import numpy as np
     import torch
 
     import inferop_amd as ia
@@ -98,10 +71,9 @@ def main():
     ia.lib()
     dev = torch.device("cuda:0")
     stream = torch.cuda.Stream(device=dev)  # default priority
-    timer = Timer(torch, stream)
+    sp = stream.cuda_stream
     gen = torch.Generator(device=dev).manual_seed(0)
     DT = ia.dtype
-    sp = stream.cuda_stream
 
     def rand_fp8(shape):
         v = torch.randint(0, 0x7E, shape, generator=gen, device=dev, dtype=torch.int32)
@@ -110,6 +82,28 @@ def main():
 
     def rand_scales(shape):
         return (torch.rand(shape, generator=gen, device=dev) * 1e-3 + 1e-4).float()
+
+    def ev():
+        return torch.cuda.Event(enable_timing=True)
+
+    def capture(fn):
+        """HIP graph of fn's launches on `stream` (warm-up runs first, eagerly,
+        so every workspace the library needs already exists)."""
+        fn()
+        stream.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            fn()
+        return g
+
+    def time_graphs(graphs, reps):
+        e0, e1 = ev(), ev()
+        e0.record(stream)
+        for i in range(reps):
+            graphs[i % len(graphs)].replay()
+        e1.record(stream)
+        e1.synchronize()
+        return e0.elapsed_time(e1) / reps  # ms per replay
 
     result = {"metric": METRIC, "n_gpus": 1, "higher_is_better": True, "scaling": "weak",
               "vs_baseline": None, "dtype": "fp8e4m3", "data": "synthetic"}
@@ -131,64 +125,74 @@ def main():
 
         def quant_call(m, k):
             q, s = AQ[(m, k)]
-            return ia.quant_fp8_per_token_group(q, s, A[(m, k)], DT.bf16, m, k, 128, sp)
+            st = ia.quant_fp8_per_token_group(q, s, A[(m, k)], DT.bf16, m, k, 128, sp)
+            assert st == 0, st
 
         def gemm_call(m, n, k, r):
             q, s = AQ[(m, k)]
             bq, bs = W[(n, k)][r % R]
-            return ia.w8a8_block_fp8_gemm(C[(m, n)], q, s, bq, bs, m, n, k, 128, 128, DT.bf16, sp)
+            st = ia.w8a8_block_fp8_gemm(C[(m, n)], q, s, bq, bs, m, n, k, 128, 128, DT.bf16, sp)
+            assert st == 0, st
 
-        def step(i):
+        def step(r):
             for (m, n, k) in cases:
                 quant_call(m, k)
-                gemm_call(m, n, k, i)
+                gemm_call(m, n, k, r)
 
-        for (m, n, k) in cases:  # correctness of the launch path before timing
-            assert quant_call(m, k) == 0 and gemm_call(m, n, k, 0) == 0
-        for i in range(args.warmup):
-            step(i)
-        stream.synchronize()
-        torch.cuda.synchronize()
-        ms_step = timer.span(lambda i: step(i + args.warmup), args.steps)
-        torch.cuda.synchronize()
+        step_graphs = [capture(lambda r=r: step(r)) for r in range(R)]
+        time_graphs(step_graphs, args.warmup)
+        ms_step = time_graphs(step_graphs, args.steps)
         value = step_bytes / (ms_step * 1e-3) / 1e9
+        # the same step launched eagerly (host launch overhead included)
+        e0, e1 = ev(), ev()
+        e0.record(stream)
+        for i in range(20):
+            step(i)
+        e1.record(stream)
+        e1.synchronize()
+        ms_step_eager = e0.elapsed_time(e1) / 20
 
-        # per-kernel durations (each launch bracketed by events)
+        # per-kernel: a graph of PER_KERNEL_LAUNCHES back-to-back launches
         detail = []
         g_bytes = g_ms = q_bytes = q_ms = 0.0
-        reps = max(20, args.steps)
         for (m, n, k) in cases:
-            qmed, qmean = timer.each(lambda i: quant_call(m, k), reps)
-            gmed, gmean = timer.each(lambda i: gemm_call(m, n, k, i), reps)
-            gb = gemm_bytes(m, n, k)
-            qb = quant_bytes(m, k)
+            gq = capture(lambda: [quant_call(m, k) for _ in range(PER_KERNEL_LAUNCHES)])
+            gg = capture(lambda: [gemm_call(m, n, k, r) for r in range(PER_KERNEL_LAUNCHES)])
+            time_graphs([gq, gg], 4)
+            qms = time_graphs([gq], 10) / PER_KERNEL_LAUNCHES
+            gms = time_graphs([gg], 10) / PER_KERNEL_LAUNCHES
+            gb, qb = gemm_bytes(m, n, k), quant_bytes(m, k)
             g_bytes += gb
-            g_ms += gmean
+            g_ms += gms
             q_bytes += qb
-            q_ms += qmean
+            q_ms += qms
             cfg, split = ia.gemm_select(m, n, k)
-            detail.append({"m": m, "n": n, "k": k, "gemm_us": round(gmean * 1e3, 2),
-                           "gemm_gbs": round(gb / (gmean * 1e-3) / 1e9, 1),
-                           "quant_us": round(qmean * 1e3, 2),
+            detail.append({"m": m, "n": n, "k": k, "gemm_us": round(gms * 1e3, 2),
+                           "gemm_gbs": round(gb / (gms * 1e-3) / 1e9, 1),
+                           "quant_us": round(qms * 1e3, 2),
                            "kernel": ia.gemm_config_name(cfg), "split_k": split})
+            del gq, gg
         gemm_gbs = g_bytes / (g_ms * 1e-3) / 1e9
         result.update({
-            "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "steps": args.steps,
+            "value": round(value, 1), "unit": "GB/s", "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
             "config": {"workload": "BASELINE configs[1] decode step: per-token-group quant of "
                                    "bf16 A[M,K] + W8A8 block-FP8 GEMM -> bf16 C[M,N], "
-                                   "M in {1,16,64} x (N,K) in {(7168,2048),(4096,7168),(2112,7168)}",
+                                   "M in {1,16,64} x (N,K) in {(7168,2048),(4096,7168),"
+                                   "(2112,7168)}; 18 launches replayed as one HIP graph",
                        "step_bytes": step_bytes, "weight_copies_rotated": R,
-                       "hbm_frac_step": round(value / HBM_PEAK_GBS, 4)},
-            "roofline": {"bound": "hbm", "kernel": "w8a8 block-FP8 GEMM (decode tiles)",
+                       "hbm_frac_step": round(value / HBM_PEAK_GBS, 4),
+                       "ms_per_step_eager_launch": round(ms_step_eager, 5)},
+            "roofline": {"bound": "hbm", "kernel": "w8a8 block-FP8 GEMM, decode tiles",
                          "achieved": round(gemm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(gemm_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                         "bytes_per_step": int(g_bytes),
+                         "algorithmic_bytes_per_step": int(g_bytes),
                          "avg_launch_us": round(g_ms / len(cases) * 1e3, 3)},
             "decode_detail": detail,
             "quant_decode_gbs": round(q_bytes / (q_ms * 1e-3) / 1e9, 1),
         })
-        del W, A, AQ, C
+        del step_graphs, W, A, AQ, C
+        torch.cuda.empty_cache()
 
         # ---------------- prefill GEMM (configs[2], M = 4096) ----------------
         pre = []
@@ -201,25 +205,32 @@ def main():
 
             def g(i, n=n, k=k, q=q, s=s, ws=ws, c=c):
                 bq, bs = ws[i % 2]
-                ia.w8a8_block_fp8_gemm(c, q, s, bq, bs, m, n, k, 128, 128, DT.bf16, sp)
+                st = ia.w8a8_block_fp8_gemm(c, q, s, bq, bs, m, n, k, 128, 128, DT.bf16, sp)
+                assert st == 0, st
 
-            for i in range(3):
-                g(i)
-            med, mean = timer.each(g, max(10, args.steps // 2))
-            tflops = 2.0 * m * n * k / (mean * 1e-3) / 1e12
+            gg = capture(lambda: [g(i) for i in range(4)])
+            time_graphs([gg], 2)
+            us = time_graphs([gg], 5) / 4 * 1e3
+            tflops = 2.0 * m * n * k / (us * 1e-6) / 1e12
             ai = 2.0 * m * n * k / gemm_bytes(m, n, k)
             bound = min(FP8_PEAK_TFLOPS, ai * HBM_PEAK_GBS / 1e3)
             cfg, split = ia.gemm_select(m, n, k)
-            pre.append({"m": m, "n": n, "k": k, "us": round(mean * 1e3, 2),
-                        "tflops": round(tflops, 1), "frac_of_peak": round(tflops / FP8_PEAK_TFLOPS, 4),
+            pre.append({"m": m, "n": n, "k": k, "us": round(us, 2), "tflops": round(tflops, 1),
+                        "frac_of_peak": round(tflops / FP8_PEAK_TFLOPS, 4),
                         "frac_of_roofline": round(tflops / bound, 4),
                         "kernel": ia.gemm_config_name(cfg), "split_k": split})
-            del a, q, s, ws, c
+            del a, q, s, ws, c, gg
         tot_flops = sum(2.0 * p["m"] * p["n"] * p["k"] for p in pre)
         tot_s = sum(p["us"] for p in pre) * 1e-6
-        result["prefill"] = {"tflops": round(tot_flops / tot_s / 1e12, 1),
-                             "frac_of_peak": round(tot_flops / tot_s / 1e12 / FP8_PEAK_TFLOPS, 4),
-                             "peak_tflops": FP8_PEAK_TFLOPS, "shapes": pre}
+        result["prefill"] = {
+            "tflops": round(tot_flops / tot_s / 1e12, 1),
+            "frac_of_peak": round(tot_flops / tot_s / 1e12 / FP8_PEAK_TFLOPS, 4),
+            "peak_tflops": FP8_PEAK_TFLOPS, "shapes": pre,
+            "roofline": {"bound": "mfma", "kernel": "w8a8 block-FP8 GEMM, prefill tiles",
+                         "achieved": round(tot_flops / tot_s / 1e12, 1),
+                         "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tot_flops / tot_s / 1e12 / FP8_PEAK_TFLOPS, 4)}}
+        torch.cuda.empty_cache()
 
         # ---------------- quantizer on large inputs ----------------
         qres = []
@@ -231,16 +242,20 @@ def main():
             s = torch.empty((mq, kq // 128), dtype=torch.float32, device=dev)
 
             def f(i, xs=xs, q=q, s=s, mq=mq, kq=kq):
-                ia.quant_fp8_per_token_group(q, s, xs[i % len(xs)], DT.bf16, mq, kq, 128, sp)
+                st = ia.quant_fp8_per_token_group(q, s, xs[i % len(xs)], DT.bf16, mq, kq, 128, sp)
+                assert st == 0, st
 
-            for i in range(3):
-                f(i)
-            med, mean = timer.each(f, max(10, args.steps // 2))
-            gbs = quant_bytes(mq, kq) / (mean * 1e-3) / 1e9
-            qres.append({"m": mq, "k": kq, "us": round(mean * 1e3, 2), "gbs": round(gbs, 1),
+            gq = capture(lambda: [f(i) for i in range(nbuf)])
+            time_graphs([gq], 2)
+            us = time_graphs([gq], 5) / nbuf * 1e3
+            gbs = quant_bytes(mq, kq) / (us * 1e-6) / 1e9
+            qres.append({"m": mq, "k": kq, "us": round(us, 2), "gbs": round(gbs, 1),
                          "frac": round(gbs / HBM_PEAK_GBS, 4)})
-            del xs, q, s
-        result["quant"] = {"shapes": qres, "peak_gbs": HBM_PEAK_GBS}
+            del xs, q, s, gq
+        result["quant"] = {"shapes": qres, "peak_gbs": HBM_PEAK_GBS,
+                           "roofline": {"bound": "hbm", "kernel": "per-token-group quantizer",
+                                        "achieved": qres[-1]["gbs"], "peak": HBM_PEAK_GBS,
+                                        "unit": "GB/s", "frac": qres[-1]["frac"]}}
 
     torch.cuda.synchronize()
     if not args.no_cpu:
@@ -284,8 +299,8 @@ def cpu_baseline():
         pass
     return {"value": round(total_bytes / t_total / 1e9, 4), "unit": "GB/s", "cores": 1,
             "kind": "reference" if use_ref else "port",
-            "sample": "the full decode workload once (9 quant + 9 GEMM, same shapes as the GPU "
-                      f"step), single thread, {t_total:.1f} s; host CPU: {cpu}",
+            "sample": "the full decode workload once (9 quant + 9 GEMM, the GPU step's shapes), "
+                      f"single thread, {t_total:.1f} s, compiled -O2; host CPU: {cpu}",
             "seconds": round(t_total, 2)}
 
 

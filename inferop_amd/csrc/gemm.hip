@@ -5,30 +5,38 @@
 //
 // Matrix cores: v_mfma_scale_f32_16x16x128_f8f6f4 with both formats E4M3 and
 // unit E8M0 scales.  One instruction multiplies a 16x128 weight slice by a
-// 16x128 activation slice, i.e. exactly one 128-wide scale group, so each
-// MFMA yields the group's partial dot products exactly as the fp8 products
-// sum in fp32; the fp32 block scales are then applied in VALU registers:
-//   acc = fma(partial, sa[m,g] * sb[n/128,g], acc)
+// 16x128 activation slice -- exactly one 128-wide scale group -- so each MFMA
+// yields the group's partial dot products, and the fp32 block scales are
+// applied in VALU registers:  acc = fma(partial, sa[m,g] * sb[n/128,g], acc).
 // The weight slice is the MFMA "A" operand and the activation slice the "B"
 // operand, so a lane's four accumulator registers are four consecutive n of
-// one output row m: one activation scale per lane per 16-row slice, and the
-// weight scale is uniform across a wave (a wave never straddles a 128-row
-// weight block) and lives in an SGPR.  The same four registers are four
-// contiguous outputs in memory, stored as one vector.
+// one output row m: one activation scale per lane per 16-row slice, one weight
+// scale per wave (a wave never straddles a 128-row weight block, the scale
+// sits in an SGPR), and the four values are contiguous in C.
 //
-// Data movement: a workgroup owns a BN x BM output tile (n x m).  Per scale
-// group it stages B[BN,128] and A[BM,128] in LDS, double-buffered: the next
-// group's global loads are in flight while the current group's MFMAs run.  An
-// LDS row is 128 bytes = eight 16-byte chunks, stored at chunk ^ (row & 7) so
-// the eight lanes of a ds_read_b128 phase hit eight different bank groups.
-// Each lane feeds the MFMA with chunks (lane/16) and (lane/16 + 4) of its
-// row; both operands use the same chunk order, so the K permutation cancels.
+// Operand layout: lane l supplies row (l % 16) of its 16-row slice and the
+// 16-byte chunks (l / 16) and (l / 16 + 4) of the 128-byte group.  Both
+// operands use the same chunk order, so the K permutation cancels.
 //
-// Split-K (small M): blockIdx.z selects a range of scale groups.  Each split
-// writes its fp32 partial tile to a library-owned workspace; the last split
-// to arrive (device-scope atomic counter) adds the partials in split order,
-// writes C and resets the counter, so results are deterministic and no block
-// ever waits on another.
+// Two kernel families:
+//
+// * decode (M <= 64 per tile, HBM-bound): no LDS for operands and no barrier
+//   in the main loop.  Each wave streams its weight rows straight from HBM
+//   into MFMA registers (non-temporal 16-byte loads, U scale groups in flight)
+//   and re-reads the small activation tile from L2.  The waves of a workgroup
+//   split the workgroup's K range and are summed through LDS; workgroups
+//   split K further (split-K) and the last one to finish a tile adds the
+//   partials in split order (deterministic).  Partials travel through
+//   device-coherent stores and loads (sc1) and a device-scope atomic counter,
+//   so no L2 writeback or invalidate is needed.
+//
+// * prefill (large M, MFMA-bound): a BN x BM output tile per workgroup, A and
+//   B staged in LDS by direct global->LDS loads (global_load_lds_dwordx4, no
+//   VGPR round trip), double-buffered so group g+1 streams in while group g is
+//   multiplied.  LDS rows are 128 bytes = eight 16-byte chunks stored at
+//   chunk ^ (row & 7): the eight lanes of a ds_read_b128 phase hit eight
+//   different bank groups.  Tiles are renumbered so each XCD works on a
+//   contiguous, M-grouped range of tiles (L2 reuse of A and B).
 #include <mutex>
 #include <unordered_map>
 
@@ -47,77 +55,293 @@ struct GemmArgs {
   float* ws;      // split-K partials
   int* counters;  // split-K arrival counters, one per output tile
   int m, n, k;
-  int split;
   int vec_ok;  // C rows can take 4-element vector stores (N % 4 == 0, C aligned)
 };
 
-__device__ __forceinline__ i32x8 lds_operand(const uint8_t* base, int row, int c0) {
-  const uint8_t* r = base + row * 128;
-  const int x = row & 7;
-  const uint4 lo = *reinterpret_cast<const uint4*>(r + ((c0 ^ x) << 4));
-  const uint4 hi = *reinterpret_cast<const uint4*>(r + ((c0 ^ x ^ 4) << 4));
+__device__ __forceinline__ f32x4 mfma_group(const i32x8& w, const i32x8& x) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w, x, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0,
+                                                          0, 127, 0, 127);
+}
+
+__device__ __forceinline__ i32x8 cat8(const u32x4& lo, const u32x4& hi) {
   return i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
                (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
 }
 
-template <int BN, int BM, int WN, int WM, int OUT_DT, bool SPLIT>
-__global__ __launch_bounds__(64 * WN * WM) void gemm_kernel(GemmArgs a) {
-  constexpr int T = 64 * WN * WM;
+// 32 operand bytes of one lane straight from global memory: chunks c0 and c0+4
+// of the 128-byte group at p (p already points at chunk c0).
+template <bool NT>
+__device__ __forceinline__ i32x8 load_operand(const uint8_t* p) {
+  const u32x4* q = reinterpret_cast<const u32x4*>(p);
+  if constexpr (NT) {
+    return cat8(__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 4));
+  } else {
+    return cat8(q[0], q[4]);
+  }
+}
+
+__device__ __forceinline__ i32x8 lds_operand(const uint8_t* base, int row, int c0) {
+  const uint8_t* r = base + row * 128;
+  const int x = row & 7;
+  const u32x4 lo = *reinterpret_cast<const u32x4*>(r + ((c0 ^ x) << 4));
+  const u32x4 hi = *reinterpret_cast<const u32x4*>(r + ((c0 ^ x ^ 4) << 4));
+  return cat8(lo, hi);
+}
+
+// Store a lane's 4 consecutive outputs of row m starting at column n.
+template <int OUT_DT>
+__device__ __forceinline__ void store_out4(const GemmArgs& a, int m, int n, const f32x4& v) {
+  using OT = typename OutT<OUT_DT>::T;
+  if (m >= a.m) return;
+  OT* dst = reinterpret_cast<OT*>(a.c) + (int64_t)m * a.n + n;
+  if (a.vec_ok && n + 3 < a.n) {
+    store4<OUT_DT>(dst, v[0], v[1], v[2], v[3]);
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (n + r < a.n) store1<OUT_DT>(dst + r, v[r]);
+  }
+}
+
+// ---- split-K fixup -------------------------------------------------------------
+// Called by every thread of a workgroup once its tile partial is complete in
+// `part` (PAIRS f32x4 per lane, pair p owned by wave p % W).  Returns true in
+// the workgroup that arrives last; `part` then holds the sum over all splits
+// in split order.
+template <int PAIRS, int W>
+__device__ __forceinline__ bool splitk_fixup(const GemmArgs& a, f32x4 (&part)[PAIRS], int split,
+                                             int z, int tile, int64_t tiles, int wave, int lane) {
+  __shared__ int s_last;
+  float* mine = a.ws + ((int64_t)z * tiles + tile) * (PAIRS * 256);
+#pragma unroll
+  for (int p = 0; p < PAIRS; ++p) {
+    if (p % W != wave) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      __hip_atomic_store(mine + (p * 64 + lane) * 4 + r, part[p][r], __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's device-coherent stores are acknowledged
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int old = __hip_atomic_fetch_add(a.counters + tile, 1, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+    s_last = (old == split - 1);
+  }
+  __syncthreads();
+  if (!s_last) return false;
+#pragma unroll
+  for (int p = 0; p < PAIRS; ++p) {
+    if (p % W != wave) continue;
+    f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int zz = 0; zz < split; ++zz) {
+      const float* src = a.ws + ((int64_t)zz * tiles + tile) * (PAIRS * 256) + (p * 64 + lane) * 4;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        sum[r] += __hip_atomic_load(src + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    part[p] = sum;
+  }
+  if (threadIdx.x == 0)
+    __hip_atomic_store(a.counters + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
+}
+
+// ---- decode kernel ---------------------------------------------------------------
+// grid: x = N tiles of 16*NT rows, y = K splits, z = M tiles of 16*MT rows.
+// W waves per workgroup split the workgroup's scale groups; U groups per batch
+// are loaded before any is multiplied.
+template <int NT, int MT, int W, int U, int OUT_DT>
+__global__ __launch_bounds__(64 * W) void gemm_decode_kernel(GemmArgs a) {
+  constexpr int PAIRS = NT * MT;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int M = a.m, N = a.n, K = a.k;
+  const int KG = K >> 7;
+  const int NB = (N + 127) >> 7;
+  const int n0 = blockIdx.x * (16 * NT);
+  const int m0 = blockIdx.z * (16 * MT);
+  const int split = gridDim.y, z = blockIdx.y;
+  const int gz0 = (int)((int64_t)z * KG / split), gz1 = (int)((int64_t)(z + 1) * KG / split);
+  const int cnt = gz1 - gz0;
+  const int gw0 = gz0 + wave * cnt / W, gw1 = gz0 + (wave + 1) * cnt / W;
+  const int rsub = lane & 15, c0 = lane >> 4;
+
+  const uint8_t* bp[NT];
+  const float* sbp[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int row = min(n0 + 16 * t + rsub, N - 1);
+    bp[t] = a.bq + (int64_t)row * K + c0 * 16;
+    const int nb = min((n0 + 16 * t) >> 7, NB - 1);
+    sbp[t] = a.bs + (int64_t)nb * KG;
+  }
+  const uint8_t* ap[MT];
+  const float* sap[MT];
+#pragma unroll
+  for (int j = 0; j < MT; ++j) {
+    const int row = min(m0 + 16 * j + rsub, M - 1);
+    ap[j] = a.aq + (int64_t)row * K + c0 * 16;
+    sap[j] = a.as + (int64_t)row * KG;
+  }
+
+  f32x4 acc[PAIRS];
+#pragma unroll
+  for (int p = 0; p < PAIRS; ++p) acc[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int g = gw0; g < gw1; g += U) {
+    i32x8 bv[U][NT], av[U][MT];
+    float sav[U][MT], sbv[U][NT];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int gg = min(g + u, gw1 - 1);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) bv[u][t] = load_operand<true>(bp[t] + gg * 128);
+#pragma unroll
+      for (int j = 0; j < MT; ++j) av[u][j] = load_operand<false>(ap[j] + gg * 128);
+#pragma unroll
+      for (int j = 0; j < MT; ++j) sav[u][j] = sap[j][gg];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) sbv[u][t] = sbp[t][gg];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (g + u < gw1) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+          for (int j = 0; j < MT; ++j) {
+            const f32x4 pv = mfma_group(bv[u][t], av[u][j]);
+            const float s = sav[u][j] * sbv[u][t];
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              acc[t * MT + j][r] = __builtin_fmaf(pv[r], s, acc[t * MT + j][r]);
+          }
+      }
+    }
+  }
+
+  // sum the W waves' partial tiles through LDS; pair p ends up in wave p % W
+  if constexpr (W > 1) {
+    __shared__ f32x4 red[W][PAIRS][64];
+#pragma unroll
+    for (int p = 0; p < PAIRS; ++p) red[wave][p][lane] = acc[p];
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < PAIRS; ++p) {
+      if (p % W != wave) continue;
+      f32x4 s = red[0][p][lane];
+#pragma unroll
+      for (int w = 1; w < W; ++w) s += red[w][p][lane];
+      acc[p] = s;
+    }
+  }
+
+  if (split > 1) {
+    const int tile = blockIdx.z * gridDim.x + blockIdx.x;
+    const int64_t tiles = (int64_t)gridDim.x * gridDim.z;
+    if (!splitk_fixup<PAIRS, W>(a, acc, split, z, tile, tiles, wave, lane)) return;
+  }
+#pragma unroll
+  for (int p = 0; p < PAIRS; ++p) {
+    if (p % W != wave) continue;
+    const int t = p / MT, j = p % MT;
+    store_out4<OUT_DT>(a, m0 + 16 * j + rsub, n0 + 16 * t + 4 * c0, acc[p]);
+  }
+}
+
+// ---- prefill kernel --------------------------------------------------------------
+// 1-D grid over output tiles; waves arranged WN (along N) x WM (along M).
+__device__ __forceinline__ void tile_of(int bid, int nblk, int tiles_n, int tiles_m, int* tn,
+                                        int* tm) {
+  // The hardware deals workgroups to the 8 XCDs round-robin; renumber so each
+  // XCD owns a contiguous range of tile ids.
+  int id = bid;
+  if ((nblk & 7) == 0) id = (bid & 7) * (nblk >> 3) + (bid >> 3);
+  // Groups of GM tile-rows along M walk across all N tiles: the A rows of a
+  // group and the B rows of the current column stay hot in L2.
+  constexpr int GM = 8;
+  const int per_group = GM * tiles_n;
+  const int grp = id / per_group;
+  const int first_m = grp * GM;
+  const int gm = min(tiles_m - first_m, GM);
+  const int in_grp = id - grp * per_group;
+  *tm = first_m + in_grp % gm;
+  *tn = in_grp / gm;
+}
+
+// s_waitcnt immediate (gfx9 encoding) that waits until at most n vector
+// memory operations of this wave are outstanding, ignoring LDS/scalar counts.
+__device__ constexpr int vmcnt_imm(int n) {
+  return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8);
+}
+
+template <int BN, int BM, int WN, int WM, int STAGES, int OUT_DT>
+__global__ __launch_bounds__(64 * WN * WM) void gemm_prefill_kernel(GemmArgs a) {
+  constexpr int NW = WN * WM;
   constexpr int TN = BN / WN, TM = BM / WM;
   constexpr int SN = TN / 16, SM = TM / 16;
-  constexpr int CB = (BN * 8 + T - 1) / T;
-  constexpr int CA = (BM * 8 + T - 1) / T;
   constexpr int kStage = (BN + BM) * 128;
+  constexpr int RB = BN / 8 / NW;  // 1 KB row blocks of B each wave loads per stage
+  constexpr int RA = BM / 8 / NW;
+  constexpr int D = STAGES - 1;               // prefetch distance in scale groups
+  constexpr int kLoadsPerStage = RB + RA + SM + 1;  // vector memory ops one stage issues
+  static_assert(STAGES >= 2 && STAGES <= 4, "2 to 4 LDS stages");
   static_assert(TN % 16 == 0 && TM % 16 == 0, "wave tile must be a multiple of 16");
   static_assert(128 % TN == 0, "a wave must stay inside one 128-row weight block");
+  static_assert(BN % (8 * NW) == 0 && BM % (8 * NW) == 0, "row blocks must split evenly");
 
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kStage];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * kStage];
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wn = wave % WN, wm = wave / WN;
   const int M = a.m, N = a.n, K = a.k;
   const int KG = K >> 7;
   const int NB = (N + 127) >> 7;
-  const int n0 = blockIdx.x * BN;
-  const int m0 = blockIdx.y * BM;
-  const int z = blockIdx.z;
-  const int g_begin = (int)((int64_t)z * KG / a.split);
-  const int g_end = (int)((int64_t)(z + 1) * KG / a.split);
+  const int tiles_n = (N + BN - 1) / BN, tiles_m = (M + BM - 1) / BM;
+  int tn, tm;
+  tile_of(blockIdx.x, gridDim.x, tiles_n, tiles_m, &tn, &tm);
+  const int n0 = tn * BN, m0 = tm * BM;
+  // tile bases are wave-uniform (SGPRs); per-lane offsets stay 32-bit
+  const uint8_t* tileB = a.bq + (int64_t)n0 * K;
+  const uint8_t* tileA = a.aq + (int64_t)m0 * K;
+  const int nlast = N - 1 - n0, mlast = M - 1 - m0;  // last valid row inside the tile
 
-  // global -> LDS staging slots (fixed per thread for the whole K loop)
-  const uint8_t* srcB[CB];
-  int ldsB[CB];
-  const uint8_t* srcA[CA];
-  int ldsA[CA];
-#pragma unroll
-  for (int s = 0; s < CB; ++s) {
-    const int idx = tid + s * T;
-    const int row = idx >> 3, c = idx & 7;
-    const int grow = min(n0 + row, N - 1);
-    srcB[s] = a.bq + (int64_t)grow * K + c * 16;
-    ldsB[s] = (idx < BN * 8) ? row * 128 + ((c ^ (row & 7)) << 4) : -1;
-  }
-#pragma unroll
-  for (int s = 0; s < CA; ++s) {
-    const int idx = tid + s * T;
-    const int row = idx >> 3, c = idx & 7;
-    const int grow = min(m0 + row, M - 1);
-    srcA[s] = a.aq + (int64_t)grow * K + c * 16;
-    ldsA[s] = (idx < BM * 8) ? BN * 128 + row * 128 + ((c ^ (row & 7)) << 4) : -1;
-  }
-
-  // scale pointers: one activation row per lane per 16-row slice, one weight
-  // block per wave.
-  const float* saP[SM];
-#pragma unroll
-  for (int j = 0; j < SM; ++j) {
-    const int mrow = min(m0 + wm * TM + 16 * j + (lane & 15), M - 1);
-    saP[j] = a.as + (int64_t)mrow * KG;
-  }
+  // direct-to-LDS slots: wave instruction r covers rows 8*(wave + r*NW) .. +8;
+  // lane -> row + (lane >> 3), chunk (lane & 7) ^ (lane >> 3)
+  const int lrow = lane >> 3;
+  const int lcol = ((lane & 7) ^ lrow) * 16;
+  const int rsub = lane & 15, c0 = lane >> 4;
+  const float* saT = a.as + (int64_t)m0 * KG;
   const int nbw = min((n0 + wn * TN) >> 7, NB - 1);
   const float* sbP = a.bs + (int64_t)nbw * KG;
+
+  // one stage = the B and A tiles of scale group g into LDS buffer `buf`,
+  // plus this lane's activation scales and the wave's weight scale of group g.
+  // The scale loads go first: the waits count vector memory operations in
+  // issue order, so a later-issued load would hold back the tiles' wait.
+  auto issue_stage = [&](int g, int buf, float* sa_dst) {
+#pragma unroll
+    for (int j = 0; j < SM; ++j) sa_dst[j] = saT[min(wm * TM + 16 * j + rsub, mlast) * KG + g];
+    sa_dst[SM] = sbP[g];
+    uint8_t* sb = smem + buf * kStage;
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const int row = min(8 * (wave + r * NW) + lrow, nlast);
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void*)(tileB + (row * K + lcol + g * 128)),
+          (__attribute__((address_space(3))) void*)(sb + 8 * (wave + r * NW) * 128), 16, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < RA; ++r) {
+      const int row = min(8 * (wave + r * NW) + lrow, mlast);
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void*)(tileA + (row * K + lcol + g * 128)),
+          (__attribute__((address_space(3))) void*)(sb + BN * 128 + 8 * (wave + r * NW) * 128),
+          16, 0, 0);
+    }
+  };
 
   f32x4 acc[SN][SM];
 #pragma unroll
@@ -125,142 +349,58 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < SM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  uint4 stB[CB], stA[CA];
-  float saN[SM], sbN = 0.f;
+  // scales of the groups in flight: sa[0] is the group being multiplied,
+  // sa[d] the group d ahead; sa[d][SM] is the weight scale
+  float sa[STAGES][SM + 1];
+#pragma unroll
+  for (int d = 0; d < D; ++d)
+    if (d < KG) issue_stage(d, d, sa[d]);
 
-  if (g_begin < g_end) {
-#pragma unroll
-    for (int s = 0; s < CB; ++s)
-      if (ldsB[s] >= 0) stB[s] = *reinterpret_cast<const uint4*>(srcB[s] + g_begin * 128);
-#pragma unroll
-    for (int s = 0; s < CA; ++s)
-      if (ldsA[s] >= 0) stA[s] = *reinterpret_cast<const uint4*>(srcA[s] + g_begin * 128);
-#pragma unroll
-    for (int j = 0; j < SM; ++j) saN[j] = saP[j][g_begin];
-    sbN = sbP[g_begin];
-#pragma unroll
-    for (int s = 0; s < CB; ++s)
-      if (ldsB[s] >= 0) *reinterpret_cast<uint4*>(smem + ldsB[s]) = stB[s];
-#pragma unroll
-    for (int s = 0; s < CA; ++s)
-      if (ldsA[s] >= 0) *reinterpret_cast<uint4*>(smem + ldsA[s]) = stA[s];
-  }
-  __syncthreads();
-
-  const int c0 = lane >> 4;
-  const int rsub = lane & 15;
-  int buf = 0;
-  for (int g = g_begin; g < g_end; ++g) {
-    float saC[SM];
-#pragma unroll
-    for (int j = 0; j < SM; ++j) saC[j] = saN[j];
-    const float sbC = sbN;
-    const bool more = g + 1 < g_end;
-    if (more) {
-#pragma unroll
-      for (int s = 0; s < CB; ++s)
-        if (ldsB[s] >= 0) stB[s] = *reinterpret_cast<const uint4*>(srcB[s] + (g + 1) * 128);
-#pragma unroll
-      for (int s = 0; s < CA; ++s)
-        if (ldsA[s] >= 0) stA[s] = *reinterpret_cast<const uint4*>(srcA[s] + (g + 1) * 128);
-#pragma unroll
-      for (int j = 0; j < SM; ++j) saN[j] = saP[j][g + 1];
-      sbN = sbP[g + 1];
+  for (int g = 0; g < KG; ++g) {
+    // stage g must have landed; the D-1 later stages may still be in flight
+    if (g + D - 1 < KG) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm((D - 1) * kLoadsPerStage));
+    } else {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     }
+    __syncthreads();  // every wave's share of stage g is in LDS; stage g-1 is consumed
+    if (g + D < KG) issue_stage(g + D, (g + D) % STAGES, sa[D]);
+    const float sbC = sa[0][SM];
 
-    const uint8_t* bB = smem + buf * kStage;
+    const uint8_t* bB = smem + (g % STAGES) * kStage;
     const uint8_t* bA = bB + BN * 128;
     i32x8 aop[SM];
 #pragma unroll
     for (int j = 0; j < SM; ++j) aop[j] = lds_operand(bA, wm * TM + 16 * j + rsub, c0);
     float sab[SM];
 #pragma unroll
-    for (int j = 0; j < SM; ++j) sab[j] = saC[j] * sbC;
+    for (int j = 0; j < SM; ++j) sab[j] = sa[0][j] * sbC;
+    // the MFMAs of weight slice i are independent of the promotion FMAs of
+    // slice i-1, so the matrix core and the VALU overlap (the scheduler
+    // interleaves them; the second wave on the SIMD fills the rest)
 #pragma unroll
     for (int i = 0; i < SN; ++i) {
       const i32x8 bop = lds_operand(bB, wn * TN + 16 * i + rsub, c0);
+      f32x4 pv[SM];
 #pragma unroll
-      for (int j = 0; j < SM; ++j) {
-        const f32x4 p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-            bop, aop[j], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(p[r], sab[j], acc[i][j][r]);
-      }
-    }
-
-    if (more) {
-      uint8_t* nb = smem + (buf ^ 1) * kStage;
-#pragma unroll
-      for (int s = 0; s < CB; ++s)
-        if (ldsB[s] >= 0) *reinterpret_cast<uint4*>(nb + ldsB[s]) = stB[s];
-#pragma unroll
-      for (int s = 0; s < CA; ++s)
-        if (ldsA[s] >= 0) *reinterpret_cast<uint4*>(nb + ldsA[s]) = stA[s];
-    }
-    __syncthreads();
-    buf ^= 1;
-  }
-
-  using OT = typename OutT<OUT_DT>::T;
-  OT* C = reinterpret_cast<OT*>(a.c);
-  const bool vec_ok = a.vec_ok != 0;
-
-  if constexpr (SPLIT) {
-    // partial tile layout: [split][tile][wave][i][j][lane][4] floats
-    const int tile = blockIdx.y * gridDim.x + blockIdx.x;
-    const int64_t tiles = (int64_t)gridDim.x * gridDim.y;
-    constexpr int kTileFloats = BN * BM;
-    float* mine = a.ws + ((int64_t)z * tiles + tile) * kTileFloats + wave * (SN * SM * 256);
-#pragma unroll
-    for (int i = 0; i < SN; ++i)
+      for (int j = 0; j < SM; ++j) pv[j] = mfma_group(bop, aop[j]);
 #pragma unroll
       for (int j = 0; j < SM; ++j)
-        *reinterpret_cast<f32x4*>(mine + ((i * SM + j) * 64 + lane) * 4) = acc[i][j];
-    __threadfence();
-    __syncthreads();
-    __shared__ int s_last;
-    if (tid == 0) {
-      const int old = atomicAdd(a.counters + tile, 1);
-      s_last = (old == a.split - 1);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(pv[j][r], sab[j], acc[i][j][r]);
     }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
 #pragma unroll
-    for (int i = 0; i < SN; ++i)
+    for (int d = 0; d < D; ++d)
 #pragma unroll
-      for (int j = 0; j < SM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int zz = 0; zz < a.split; ++zz) {
-      const float* part = a.ws + ((int64_t)zz * tiles + tile) * kTileFloats + wave * (SN * SM * 256);
-#pragma unroll
-      for (int i = 0; i < SN; ++i)
-#pragma unroll
-        for (int j = 0; j < SM; ++j) {
-          const f32x4 v = __builtin_nontemporal_load(
-              reinterpret_cast<const f32x4*>(part + ((i * SM + j) * 64 + lane) * 4));
-          acc[i][j] += v;
-        }
-    }
-    if (tid == 0) a.counters[tile] = 0;
+      for (int j = 0; j <= SM; ++j) sa[d][j] = sa[d + 1][j];
   }
 
 #pragma unroll
-  for (int j = 0; j < SM; ++j) {
-    const int m = m0 + wm * TM + 16 * j + rsub;
-    if (m >= M) continue;
+  for (int i = 0; i < SN; ++i)
 #pragma unroll
-    for (int i = 0; i < SN; ++i) {
-      const int n = n0 + wn * TN + 16 * i + 4 * c0;
-      OT* dst = C + (int64_t)m * N + n;
-      if (vec_ok && n + 3 < N) {
-        store4<OUT_DT>(dst, acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (n + r < N) store1<OUT_DT>(dst + r, acc[i][j][r]);
-      }
-    }
-  }
+    for (int j = 0; j < SM; ++j)
+      store_out4<OUT_DT>(a, m0 + wm * TM + 16 * j + rsub, n0 + wn * TN + 16 * i + 4 * c0,
+                         acc[i][j]);
 }
 
 // ---- kernel table -------------------------------------------------------------
@@ -268,24 +408,34 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_kernel(GemmArgs a) {
 using KernelFn = void (*)(GemmArgs);
 
 struct CfgEntry {
-  int bn, bm, wn, wm;
+  int kind;  // 1 = decode, 2 = prefill
+  int bn, bm, waves;
   const char* name;
-  KernelFn fn[3][2];  // [out_dt][split]
+  KernelFn fn[3];  // [out_dt index]
 };
 
-#define INFEROP_GEMM_CFG(BN, BM, WN, WM, NAME)                                                 \
-  {BN, BM, WN, WM, NAME,                                                                       \
-   {{gemm_kernel<BN, BM, WN, WM, kFp32, false>, gemm_kernel<BN, BM, WN, WM, kFp32, true>},     \
-    {gemm_kernel<BN, BM, WN, WM, kFp16, false>, gemm_kernel<BN, BM, WN, WM, kFp16, true>},     \
-    {gemm_kernel<BN, BM, WN, WM, kBf16, false>, gemm_kernel<BN, BM, WN, WM, kBf16, true>}}}
+#define DECODE_CFG(NT, MT, W, U, NAME)                                                        \
+  {1, 16 * NT, 16 * MT, W, NAME,                                                               \
+   {gemm_decode_kernel<NT, MT, W, U, kFp32>, gemm_decode_kernel<NT, MT, W, U, kFp16>,          \
+    gemm_decode_kernel<NT, MT, W, U, kBf16>}}
+#define PREFILL_CFG(BN, BM, WN, WM, ST, NAME)                                                 \
+  {2, BN, BM, WN * WM, NAME,                                                                   \
+   {gemm_prefill_kernel<BN, BM, WN, WM, ST, kFp32>,                                            \
+    gemm_prefill_kernel<BN, BM, WN, WM, ST, kFp16>,                                            \
+    gemm_prefill_kernel<BN, BM, WN, WM, ST, kBf16>}}
 
 const CfgEntry kCfgs[] = {
-    INFEROP_GEMM_CFG(128, 128, 2, 2, "n128_m128_w2x2"),
-    INFEROP_GEMM_CFG(64, 16, 4, 1, "n64_m16_w4x1"),
-    INFEROP_GEMM_CFG(64, 32, 4, 1, "n64_m32_w4x1"),
-    INFEROP_GEMM_CFG(64, 64, 4, 1, "n64_m64_w4x1"),
-    INFEROP_GEMM_CFG(256, 128, 2, 2, "n256_m128_w2x2"),
-    INFEROP_GEMM_CFG(128, 256, 2, 2, "n128_m256_w2x2"),
+    DECODE_CFG(1, 1, 16, 4, "dec_n16_m16_w16"),
+    DECODE_CFG(1, 1, 8, 4, "dec_n16_m16_w8"),
+    DECODE_CFG(1, 2, 16, 4, "dec_n16_m32_w16"),
+    DECODE_CFG(1, 4, 16, 2, "dec_n16_m64_w16"),
+    DECODE_CFG(2, 4, 8, 2, "dec_n32_m64_w8"),
+    DECODE_CFG(2, 1, 8, 4, "dec_n32_m16_w8"),
+    PREFILL_CFG(256, 128, 4, 2, 3, "pre_n256_m128_w8_s3"),
+    PREFILL_CFG(128, 256, 2, 4, 3, "pre_n128_m256_w8_s3"),
+    PREFILL_CFG(128, 128, 2, 2, 2, "pre_n128_m128_w4_s2"),
+    PREFILL_CFG(128, 128, 2, 2, 4, "pre_n128_m128_w4_s4"),
+    PREFILL_CFG(256, 256, 2, 4, 2, "pre_n256_m256_w8_s2"),
 };
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
@@ -369,8 +519,8 @@ extern "C" int inferop_hip_gemm_config_info(int32_t cfg, inferop_gemm_cfg_info* 
   if (cfg < 0 || cfg >= kNumCfgs || !info) return hipErrorInvalidValue;
   info->bn = kCfgs[cfg].bn;
   info->bm = kCfgs[cfg].bm;
-  info->waves = kCfgs[cfg].wn * kCfgs[cfg].wm;
-  info->kind = 0;
+  info->waves = kCfgs[cfg].waves;
+  info->kind = kCfgs[cfg].kind;
   info->name = kCfgs[cfg].name;
   return hipSuccess;
 }
@@ -385,24 +535,29 @@ extern "C" int inferop_hip_gemm_w8a8_block(void* c, const uint8_t* a_q, const fl
   if (m > 0x7FFFFFFF || n > 0x7FFFFFFF || k > 0x7FFFFFFF) return hipErrorInvalidValue;
   const CfgEntry& cf = kCfgs[launch->cfg];
   const int kg = (int)(k / 128);
-  int split = launch->split_k < 1 ? 1 : launch->split_k;
-  if (split > kg) split = kg;
   const int64_t tn = (n + cf.bn - 1) / cf.bn;
   const int64_t tm = (m + cf.bm - 1) / cf.bm;
-  if (tn > 0x7FFFFFFF || tm > 65535 || split > 65535) return hipErrorInvalidConfiguration;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int out_bytes = out_dt == kFp32 ? 4 : 2;
   const int vec_ok = (n % 4 == 0) && ((uintptr_t)c % (size_t)(4 * out_bytes) == 0);
   GemmArgs args{c,       a_q,    a_scales, b_q,    b_scales, nullptr,
-                nullptr, (int)m, (int)n,   (int)k, split,    vec_ok};
-  if (split > 1) {
-    const size_t tiles = (size_t)(tn * tm);
-    const size_t bytes = (size_t)split * tiles * (size_t)cf.bn * (size_t)cf.bm * sizeof(float);
-    hipError_t e = get_workspace(st, bytes, tiles, &args.ws, &args.counters);
-    if (e != hipSuccess) return e;
+                nullptr, (int)m, (int)n,   (int)k, vec_ok};
+  if (cf.kind == 1) {
+    int split = launch->split_k < 1 ? 1 : launch->split_k;
+    if (split > kg) split = kg;
+    if (tn > 0x7FFFFFFF || split > 65535 || tm > 65535) return hipErrorInvalidConfiguration;
+    if (split > 1) {
+      const size_t tiles = (size_t)(tn * tm);
+      const size_t bytes = (size_t)split * tiles * (size_t)cf.bn * (size_t)cf.bm * sizeof(float);
+      hipError_t e = get_workspace(st, bytes, tiles, &args.ws, &args.counters);
+      if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(cf.fn[di], dim3((unsigned)tn, (unsigned)split, (unsigned)tm),
+                       dim3(64 * cf.waves), 0, st, args);
+  } else {
+    const int64_t tiles = tn * tm;
+    if (tiles > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL(cf.fn[di], dim3((unsigned)tiles), dim3(64 * cf.waves), 0, st, args);
   }
-  const dim3 grid((unsigned)tn, (unsigned)tm, (unsigned)split);
-  const dim3 block(64 * cf.wn * cf.wm);
-  hipLaunchKernelGGL(cf.fn[di][split > 1 ? 1 : 0], grid, block, 0, st, args);
   return hipGetLastError();
 }

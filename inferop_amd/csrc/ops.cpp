@@ -63,12 +63,17 @@ int status_of_hip(int e) { return e == 0 ? INFEROP_OK : INFEROP_ERR_LAUNCH; }
 // ---- gfx950 tile selection ----------------------------------------------------
 // Kernel table indices (inferop_amd/csrc/gemm.hip, kCfgs).
 enum GemmCfg : int32_t {
-  kN128M128 = 0,
-  kN64M16 = 1,
-  kN64M32 = 2,
-  kN64M64 = 3,
-  kN256M128 = 4,
-  kN128M256 = 5,
+  kDecN16M16W16 = 0,
+  kDecN16M16W8 = 1,
+  kDecN16M32W16 = 2,
+  kDecN16M64W16 = 3,
+  kDecN32M64W8 = 4,
+  kDecN32M16W8 = 5,
+  kPreN256M128S3 = 6,
+  kPreN128M256S3 = 7,
+  kPreN128M128S2 = 8,
+  kPreN128M128S4 = 9,
+  kPreN256M256S2 = 10,
 };
 
 struct GemmChoice {
@@ -79,32 +84,32 @@ struct GemmChoice {
 GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
   if (cus <= 0) cus = 256;
   const int64_t kg = k / 128;
-  int32_t cfg;
-  int64_t bn, bm;
-  if (m <= 16) {
-    cfg = kN64M16, bn = 64, bm = 16;
-  } else if (m <= 32) {
-    cfg = kN64M32, bn = 64, bm = 32;
-  } else if (m <= 64) {
-    cfg = kN64M64, bn = 64, bm = 64;
-  } else {
-    cfg = kN128M128, bn = 128, bm = 128;
+  if (m <= 64) {
+    // HBM-bound: waves own 16 (or 32) weight rows and a few scale groups and
+    // issue all of their loads at once; the workgroup's waves split K so the
+    // weight matrix is streamed by thousands of waves in flight.  Split K
+    // across workgroups only when the N tiles alone cannot occupy the CUs.
+    int32_t cfg;
+    int64_t rows;
+    if (m <= 16) {
+      cfg = kDecN16M16W16, rows = 16;
+    } else if (m <= 32) {
+      cfg = kDecN16M32W16, rows = 16;
+    } else {
+      cfg = kDecN32M64W8, rows = 32;
+    }
+    const int64_t tiles = (n + rows - 1) / rows;
+    int64_t split = 1;
+    if (tiles < cus) split = (cus + tiles - 1) / tiles;
+    if (split > kg / 8) split = kg / 8;
+    if (split < 1) split = 1;
+    return {cfg, int32_t(split)};
   }
-  const int64_t tiles = ((n + bn - 1) / bn) * ((m + bm - 1) / bm);
-  int64_t split = 1;
-  if (bm <= 64) {
-    // HBM-bound decode shapes: enough workgroups to keep every CU streaming
-    // weights, at least two scale groups per split.
-    const int64_t want = 2 * int64_t(cus);
-    split = (want + tiles - 1) / tiles;
-    if (split > kg / 2) split = kg / 2;
-    if (split > 16) split = 16;
-  } else if (tiles < cus) {
-    split = (cus + tiles - 1) / tiles;
-    if (split > kg / 4) split = kg / 4;
-  }
-  if (split < 1) split = 1;
-  return {cfg, int32_t(split)};
+  // MFMA-bound: 256x256 tiles when they give every CU a workgroup, else the
+  // 128x128 tile (two workgroups per CU).
+  const int64_t t256 = ((n + 255) / 256) * ((m + 255) / 256);
+  if (t256 >= cus) return {kPreN256M256S2, 1};
+  return {kPreN128M128S2, 1};
 }
 
 // ---- implementations shared by the C++ and C entry points --------------------

@@ -62,9 +62,11 @@ def activations(m: int, k: int, seed: int, dist: str = "normal") -> np.ndarray:
         return g.standard_normal((m, k), dtype=np.float32)
     if dist == "stress":
         x = (4.0 * g.standard_t(3, size=(m, k))).astype(np.float32)
-        groups = x.reshape(m, k // 128, 128)
-        zero = g.random((m, k // 128)) < 0.01
+        kg = k // 128
+        groups = x[:, :kg * 128].reshape(m, kg, 128)
+        zero = g.random((m, kg)) < 0.01
         groups[zero] = 0.0
+        x[:, :kg * 128] = groups.reshape(m, kg * 128)
         out = g.random((m, k)) < 0.001
         sign = np.where(g.random((m, k)) < 0.5, -1.0, 1.0).astype(np.float32)
         x[out] = 1792.0 * sign[out]

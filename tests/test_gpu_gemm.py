@@ -137,8 +137,11 @@ def test_config3_m_sweep_sampled(m, nk):
         _check_sampled(a, aq, as_, bq, bs, c, rows, f"config3 {m}x{n}x{k} {out}")
 
 
+N_CONFIGS = inferop_amd.gemm_num_configs()
+
+
 @pytest.mark.gpu
-@pytest.mark.parametrize("config", range(6))
+@pytest.mark.parametrize("config", range(N_CONFIGS))
 @pytest.mark.parametrize("split", [1, 3])
 def test_every_kernel_config_ragged(config, split):
     device()
@@ -162,14 +165,22 @@ def test_output_dtypes_and_odd_n():
 
 
 @pytest.mark.gpu
-def test_split_k_deterministic_and_repeatable():
+@pytest.mark.parametrize("m", [1, 16, 64])
+def test_split_k_deterministic_and_repeatable(m):
+    # the split-K partials cross workgroups (and XCDs) through device-coherent
+    # stores; repeated runs must agree bit for bit with each other and, in
+    # tolerance, with the oracle, for every split count
     device()
-    m, n, k = 16, 4096, 7168
+    n, k = 2112, 7168
     _, aq, as_, bq, bs = _host_case(m, n, k, seed=9)
+    want = oracle.gemm(aq, as_, bq, bs)
     args = [to_dev(v) for v in (aq, as_, bq, bs)]
-    first = to_np(_gemm(*args, m, n, k))
-    for _ in range(3):
-        assert np.array_equal(to_np(_gemm(*args, m, n, k)), first)
+    cfg, _ = inferop_amd.gemm_select(m, n, k)
+    for split in (2, 5, 14, 56):
+        first = to_np(_gemm(*args, m, n, k, "fp32", cfg, split))
+        assert_gemm_close(first, want, f"split {split}")
+        for _ in range(5):
+            assert np.array_equal(to_np(_gemm(*args, m, n, k, "fp32", cfg, split)), first)
 
 
 @pytest.mark.gpu
