@@ -58,6 +58,22 @@ struct GemmArgs {
   int vec_ok;  // C rows can take 4-element vector stores (N % 4 == 0, C aligned)
 };
 
+// Raw buffer resource over `bytes` bytes at base (stride 0; dword3 selects a
+// 32-bit data format so untyped loads are valid).  Loads at offsets >= bytes
+// return zeros, which is how tiles past the last row of A or B are padded.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+// 16 bytes per lane from the buffer at voffset + soffset into LDS at
+// lds + 16 * lane (the LDS address is wave-uniform).
+__device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t r, void* lds, int voffset,
+                                                int soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16,
+                                           voffset, soffset, 0, 0);
+}
+
 __device__ __forceinline__ f32x4 mfma_group(const i32x8& w, const i32x8& x) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w, x, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0,
                                                           0, 127, 0, 127);
@@ -104,21 +120,25 @@ __device__ __forceinline__ void store_out4(const GemmArgs& a, int m, int n, cons
 }
 
 // ---- split-K fixup -------------------------------------------------------------
-// Called by every thread of a workgroup once its tile partial is complete in
-// `part` (PAIRS f32x4 per lane, pair p owned by wave p % W).  Returns true in
-// the workgroup that arrives last; `part` then holds the sum over all splits
-// in split order.
-template <int PAIRS, int W>
-__device__ __forceinline__ bool splitk_fixup(const GemmArgs& a, f32x4 (&part)[PAIRS], int split,
-                                             int z, int tile, int64_t tiles, int wave, int lane) {
+// Called by every thread of a workgroup once its share of the tile partial is
+// complete: this wave holds LP pairs (an f32x4 per lane each) that are pairs
+// pair_base .. pair_base+LP-1 of the tile's `pairs` pairs; valid(q) says
+// whether this lane's q-th pair carries data (inside M, owned by this wave).
+// Returns true in the workgroup that arrives last for the tile; `part` then
+// holds the sum over all splits, added in split order.
+template <int LP, typename Valid>
+__device__ __forceinline__ bool splitk_fixup(const GemmArgs& a, f32x4 (&part)[LP], int split,
+                                             int z, int tile, int64_t tiles, int pairs,
+                                             int pair_base, int lane, Valid valid) {
   __shared__ int s_last;
-  float* mine = a.ws + ((int64_t)z * tiles + tile) * (PAIRS * 256);
+  const int64_t tile_floats = (int64_t)pairs * 256;
+  float* mine = a.ws + ((int64_t)z * tiles + tile) * tile_floats + (int64_t)pair_base * 256;
 #pragma unroll
-  for (int p = 0; p < PAIRS; ++p) {
-    if (p % W != wave) continue;
+  for (int q = 0; q < LP; ++q) {
+    if (!valid(q)) continue;
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      __hip_atomic_store(mine + (p * 64 + lane) * 4 + r, part[p][r], __ATOMIC_RELAXED,
+      __hip_atomic_store(mine + (q * 64 + lane) * 4 + r, part[q][r], __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
   }
   __builtin_amdgcn_s_waitcnt(0);  // this wave's device-coherent stores are acknowledged
@@ -131,16 +151,17 @@ __device__ __forceinline__ bool splitk_fixup(const GemmArgs& a, f32x4 (&part)[PA
   __syncthreads();
   if (!s_last) return false;
 #pragma unroll
-  for (int p = 0; p < PAIRS; ++p) {
-    if (p % W != wave) continue;
+  for (int q = 0; q < LP; ++q) {
+    if (!valid(q)) continue;
     f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int zz = 0; zz < split; ++zz) {
-      const float* src = a.ws + ((int64_t)zz * tiles + tile) * (PAIRS * 256) + (p * 64 + lane) * 4;
+      const float* src = a.ws + ((int64_t)zz * tiles + tile) * tile_floats +
+                         (int64_t)pair_base * 256 + (q * 64 + lane) * 4;
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         sum[r] += __hip_atomic_load(src + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    part[p] = sum;
+    part[q] = sum;
   }
   if (threadIdx.x == 0)
     __hip_atomic_store(a.counters + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -148,34 +169,40 @@ __device__ __forceinline__ bool splitk_fixup(const GemmArgs& a, f32x4 (&part)[PA
 }
 
 // ---- decode kernel ---------------------------------------------------------------
-// grid: x = N tiles of 16*NT rows, y = K splits, z = M tiles of 16*MT rows.
-// W waves per workgroup split the workgroup's scale groups; U groups per batch
-// are loaded before any is multiplied.
-template <int NT, int MT, int W, int U, int OUT_DT>
-__global__ __launch_bounds__(64 * W) void gemm_decode_kernel(GemmArgs a) {
-  constexpr int PAIRS = NT * MT;
+// grid: x = N tiles of 16 rows, y = K splits, z = M tiles of 16*MT rows.
+// The WK waves of a workgroup split the workgroup's scale groups.  A wave
+// streams its 16 weight rows for up to U groups at a time with direct
+// global->LDS loads into its own LDS region -- each load instruction reads 8
+// whole 128-byte rows, the contiguous pattern HBM streams best -- while the
+// activation slices come from L2 straight into registers; then it reads the
+// weight operands back in MFMA layout (no barrier: the region is private).
+// The WK slices are summed through LDS; K splits across workgroups go
+// through the split-K fixup.
+template <int MT, int WK, int U, int OUT_DT>
+__global__ __launch_bounds__(64 * WK) void gemm_decode_kernel(GemmArgs a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t bst[WK][U][2048];
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wk = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int M = a.m, N = a.n, K = a.k;
   const int KG = K >> 7;
   const int NB = (N + 127) >> 7;
-  const int n0 = blockIdx.x * (16 * NT);
+  const int n0 = blockIdx.x * 16;
   const int m0 = blockIdx.z * (16 * MT);
   const int split = gridDim.y, z = blockIdx.y;
   const int gz0 = (int)((int64_t)z * KG / split), gz1 = (int)((int64_t)(z + 1) * KG / split);
   const int cnt = gz1 - gz0;
-  const int gw0 = gz0 + wave * cnt / W, gw1 = gz0 + (wave + 1) * cnt / W;
+  const int gw0 = gz0 + wk * cnt / WK, gw1 = gz0 + (wk + 1) * cnt / WK;
   const int rsub = lane & 15, c0 = lane >> 4;
 
-  const uint8_t* bp[NT];
-  const float* sbp[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    const int row = min(n0 + 16 * t + rsub, N - 1);
-    bp[t] = a.bq + (int64_t)row * K + c0 * 16;
-    const int nb = min((n0 + 16 * t) >> 7, NB - 1);
-    sbp[t] = a.bs + (int64_t)nb * KG;
-  }
+  // DMA slots: instruction i of a group covers rows 8i .. 8i+7; lane -> row
+  // 8i + (lane >> 3), 16-byte chunk (lane & 7) ^ (lane >> 3)
+  const int lrow = lane >> 3;
+  const int lcol = ((lane & 7) ^ lrow) * 16;
+  const uint8_t* tileB = a.bq + (int64_t)n0 * K;
+  const int nlast = N - 1 - n0;
+  const int off0 = min(lrow, nlast) * K + lcol;
+  const int off1 = min(8 + lrow, nlast) * K + lcol;
+  const float* sbp = a.bs + (int64_t)min(n0 >> 7, NB - 1) * KG;
   const uint8_t* ap[MT];
   const float* sap[MT];
 #pragma unroll
@@ -185,68 +212,73 @@ __global__ __launch_bounds__(64 * W) void gemm_decode_kernel(GemmArgs a) {
     sap[j] = a.as + (int64_t)row * KG;
   }
 
-  f32x4 acc[PAIRS];
+  f32x4 acc[MT];
 #pragma unroll
-  for (int p = 0; p < PAIRS; ++p) acc[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < MT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   for (int g = gw0; g < gw1; g += U) {
-    i32x8 bv[U][NT], av[U][MT];
-    float sav[U][MT], sbv[U][NT];
+    i32x8 av[U][MT];
+    float sav[U][MT], sbv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int gg = min(g + u, gw1 - 1);
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void*)(tileB + (off0 + gg * 128)),
+          (__attribute__((address_space(3))) void*)(&bst[wk][u][0]), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void*)(tileB + (off1 + gg * 128)),
+          (__attribute__((address_space(3))) void*)(&bst[wk][u][1024]), 16, 0, 0);
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int gg = min(g + u, gw1 - 1);
 #pragma unroll
-      for (int t = 0; t < NT; ++t) bv[u][t] = load_operand<true>(bp[t] + gg * 128);
-#pragma unroll
       for (int j = 0; j < MT; ++j) av[u][j] = load_operand<false>(ap[j] + gg * 128);
 #pragma unroll
       for (int j = 0; j < MT; ++j) sav[u][j] = sap[j][gg];
-#pragma unroll
-      for (int t = 0; t < NT; ++t) sbv[u][t] = sbp[t][gg];
+      sbv[u] = sbp[gg];
     }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's rows are in its LDS region
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (g + u < gw1) {
+        const i32x8 bv = lds_operand(&bst[wk][u][0], rsub, c0);
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
+        for (int j = 0; j < MT; ++j) {
+          const f32x4 pv = mfma_group(bv, av[u][j]);
+          const float s = sav[u][j] * sbv[u];
 #pragma unroll
-          for (int j = 0; j < MT; ++j) {
-            const f32x4 pv = mfma_group(bv[u][t], av[u][j]);
-            const float s = sav[u][j] * sbv[u][t];
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              acc[t * MT + j][r] = __builtin_fmaf(pv[r], s, acc[t * MT + j][r]);
-          }
+          for (int r = 0; r < 4; ++r) acc[j][r] = __builtin_fmaf(pv[r], s, acc[j][r]);
+        }
       }
     }
   }
 
-  // sum the W waves' partial tiles through LDS; pair p ends up in wave p % W
-  if constexpr (W > 1) {
-    __shared__ f32x4 red[W][PAIRS][64];
+  // sum the WK slices through LDS: wave 0 ends up with the tile
+  if constexpr (WK > 1) {
+    __shared__ f32x4 red[WK - 1][MT][64];
+    if (wk > 0) {
 #pragma unroll
-    for (int p = 0; p < PAIRS; ++p) red[wave][p][lane] = acc[p];
+      for (int j = 0; j < MT; ++j) red[wk - 1][j][lane] = acc[j];
+    }
     __syncthreads();
+    if (wk == 0) {
 #pragma unroll
-    for (int p = 0; p < PAIRS; ++p) {
-      if (p % W != wave) continue;
-      f32x4 s = red[0][p][lane];
+      for (int w = 0; w < WK - 1; ++w)
 #pragma unroll
-      for (int w = 1; w < W; ++w) s += red[w][p][lane];
-      acc[p] = s;
+        for (int j = 0; j < MT; ++j) acc[j] += red[w][j][lane];
     }
   }
 
   if (split > 1) {
     const int tile = blockIdx.z * gridDim.x + blockIdx.x;
     const int64_t tiles = (int64_t)gridDim.x * gridDim.z;
-    if (!splitk_fixup<PAIRS, W>(a, acc, split, z, tile, tiles, wave, lane)) return;
+    auto valid = [&](int q) { return wk == 0 && m0 + 16 * q + rsub < M; };
+    if (!splitk_fixup<MT>(a, acc, split, z, tile, tiles, MT, 0, lane, valid)) return;
   }
+  if (wk == 0) {
 #pragma unroll
-  for (int p = 0; p < PAIRS; ++p) {
-    if (p % W != wave) continue;
-    const int t = p / MT, j = p % MT;
-    store_out4<OUT_DT>(a, m0 + 16 * j + rsub, n0 + 16 * t + 4 * c0, acc[p]);
+    for (int j = 0; j < MT; ++j) store_out4<OUT_DT>(a, m0 + 16 * j + rsub, n0 + 4 * c0, acc[j]);
   }
 }
 
@@ -270,10 +302,22 @@ __device__ __forceinline__ void tile_of(int bid, int nblk, int tiles_n, int tile
   *tn = in_grp / gm;
 }
 
-// s_waitcnt immediate (gfx9 encoding) that waits until at most n vector
-// memory operations of this wave are outstanding, ignoring LDS/scalar counts.
-__device__ constexpr int vmcnt_imm(int n) {
-  return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8);
+// s_waitcnt immediate (gfx9 encoding): at most n vector memory operations of
+// this wave outstanding and every LDS/scalar access completed.
+__device__ constexpr int vmcnt_lgkm0_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4); }
+
+// Workgroup barrier for the LDS pipeline: wait until this wave's stage loads
+// (all but the newest n vector memory operations) have landed in LDS and its
+// LDS reads are done, then s_barrier.  Unlike __syncthreads() it does not
+// wait for every outstanding global load, so later stages stay in flight.
+// The empty asm statements keep the compiler from moving memory accesses
+// across the barrier.
+template <int N>
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm(N));
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 template <int BN, int BM, int WN, int WM, int STAGES, int OUT_DT>
@@ -281,15 +325,20 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_prefill_kernel(GemmArgs a) 
   constexpr int NW = WN * WM;
   constexpr int TN = BN / WN, TM = BM / WM;
   constexpr int SN = TN / 16, SM = TM / 16;
-  constexpr int kStage = (BN + BM) * 128;
+  // one stage in LDS: B tile | A tile | activation scales | weight scale
+  constexpr int kOffA = BN * 128;
+  constexpr int kOffSA = (BN + BM) * 128;
+  constexpr int kOffSB = kOffSA + BM * 4;
+  constexpr int kStage = ((kOffSB + 256) + 1023) / 1024 * 1024;
   constexpr int RB = BN / 8 / NW;  // 1 KB row blocks of B each wave loads per stage
   constexpr int RA = BM / 8 / NW;
-  constexpr int D = STAGES - 1;               // prefetch distance in scale groups
-  constexpr int kLoadsPerStage = RB + RA + SM + 1;  // vector memory ops one stage issues
+  constexpr int kLoadsPerStage = RB + RA + 1;  // + one scale load per wave
+  constexpr int D = STAGES - 1;                // prefetch distance in scale groups
   static_assert(STAGES >= 2 && STAGES <= 4, "2 to 4 LDS stages");
   static_assert(TN % 16 == 0 && TM % 16 == 0, "wave tile must be a multiple of 16");
   static_assert(128 % TN == 0, "a wave must stay inside one 128-row weight block");
   static_assert(BN % (8 * NW) == 0 && BM % (8 * NW) == 0, "row blocks must split evenly");
+  static_assert(BM % 64 == 0 && BM / 64 < NW, "activation scales take BM/64 waves, sb one more");
 
   __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * kStage];
 
@@ -303,44 +352,52 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_prefill_kernel(GemmArgs a) 
   int tn, tm;
   tile_of(blockIdx.x, gridDim.x, tiles_n, tiles_m, &tn, &tm);
   const int n0 = tn * BN, m0 = tm * BM;
-  // tile bases are wave-uniform (SGPRs); per-lane offsets stay 32-bit
-  const uint8_t* tileB = a.bq + (int64_t)n0 * K;
-  const uint8_t* tileA = a.aq + (int64_t)m0 * K;
-  const int nlast = N - 1 - n0, mlast = M - 1 - m0;  // last valid row inside the tile
+  // split-K: blockIdx.y selects a contiguous range of scale groups
+  const int split = gridDim.y, z = blockIdx.y;
+  const int gb = (int)((int64_t)z * KG / split), ge = (int)((int64_t)(z + 1) * KG / split);
+  const int NG = ge - gb;
+  // tile buffers: rows past the last row of A or B read as zeros
+  const int nrows = min(BN, N - n0), mrows = min(BM, M - m0);
+  const __amdgpu_buffer_rsrc_t rB = make_rsrc(a.bq + (int64_t)n0 * K, (uint32_t)(nrows * K));
+  const __amdgpu_buffer_rsrc_t rA = make_rsrc(a.aq + (int64_t)m0 * K, (uint32_t)(mrows * K));
+  const int mlast = M - 1 - m0;  // last valid row inside the tile
 
   // direct-to-LDS slots: wave instruction r covers rows 8*(wave + r*NW) .. +8;
-  // lane -> row + (lane >> 3), chunk (lane & 7) ^ (lane >> 3)
+  // lane -> row + (lane >> 3), chunk (lane & 7) ^ (lane >> 3).  The per-lane
+  // offset is the same for every instruction; the row block and the scale
+  // group go into the scalar offset.
   const int lrow = lane >> 3;
-  const int lcol = ((lane & 7) ^ lrow) * 16;
+  const int loff = lrow * K + ((lane & 7) ^ lrow) * 16;
   const int rsub = lane & 15, c0 = lane >> 4;
-  const float* saT = a.as + (int64_t)m0 * KG;
-  const int nbw = min((n0 + wn * TN) >> 7, NB - 1);
-  const float* sbP = a.bs + (int64_t)nbw * KG;
+  // scale loads: waves 0 .. BM/64-1 fetch 64 activation scales each (one per
+  // lane, row wave*64 + lane), the other waves fetch the weight scale of the
+  // tile's first 128-row block (every wave of the tile shares it when BN <=
+  // 128; otherwise each wave reads its own block's scale, see below)
+  const bool sa_wave = wave < BM / 64;
+  const float* scale_src;
+  int scale_dst;
+  if (sa_wave) {
+    scale_src = a.as + (int64_t)(m0 + min(wave * 64 + lane, mlast)) * KG;
+    scale_dst = kOffSA + wave * 256;
+  } else {
+    // lanes 0..BN/128-1 fetch the weight scales of the tile's blocks
+    const int nb = min((n0 >> 7) + min(lane, BN / 128 - 1), NB - 1);
+    scale_src = a.bs + (int64_t)nb * KG;
+    scale_dst = kOffSB;
+  }
 
-  // one stage = the B and A tiles of scale group g into LDS buffer `buf`,
-  // plus this lane's activation scales and the wave's weight scale of group g.
-  // The scale loads go first: the waits count vector memory operations in
-  // issue order, so a later-issued load would hold back the tiles' wait.
-  auto issue_stage = [&](int g, int buf, float* sa_dst) {
-#pragma unroll
-    for (int j = 0; j < SM; ++j) sa_dst[j] = saT[min(wm * TM + 16 * j + rsub, mlast) * KG + g];
-    sa_dst[SM] = sbP[g];
+  auto issue_stage = [&](int g, int buf) {
     uint8_t* sb = smem + buf * kStage;
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(scale_src + g),
+                                     (__attribute__((address_space(3))) void*)(sb + scale_dst), 4,
+                                     0, 0);
 #pragma unroll
-    for (int r = 0; r < RB; ++r) {
-      const int row = min(8 * (wave + r * NW) + lrow, nlast);
-      __builtin_amdgcn_global_load_lds(
-          (const __attribute__((address_space(1))) void*)(tileB + (row * K + lcol + g * 128)),
-          (__attribute__((address_space(3))) void*)(sb + 8 * (wave + r * NW) * 128), 16, 0, 0);
-    }
+    for (int r = 0; r < RB; ++r)
+      buffer_to_lds16(rB, sb + 8 * (wave + r * NW) * 128, loff, 8 * (wave + r * NW) * K + g * 128);
 #pragma unroll
-    for (int r = 0; r < RA; ++r) {
-      const int row = min(8 * (wave + r * NW) + lrow, mlast);
-      __builtin_amdgcn_global_load_lds(
-          (const __attribute__((address_space(1))) void*)(tileA + (row * K + lcol + g * 128)),
-          (__attribute__((address_space(3))) void*)(sb + BN * 128 + 8 * (wave + r * NW) * 128),
-          16, 0, 0);
-    }
+    for (int r = 0; r < RA; ++r)
+      buffer_to_lds16(rA, sb + kOffA + 8 * (wave + r * NW) * 128, loff,
+                      8 * (wave + r * NW) * K + g * 128);
   };
 
   f32x4 acc[SN][SM];
@@ -349,58 +406,116 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_prefill_kernel(GemmArgs a) 
 #pragma unroll
     for (int j = 0; j < SM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // scales of the groups in flight: sa[0] is the group being multiplied,
-  // sa[d] the group d ahead; sa[d][SM] is the weight scale
-  float sa[STAGES][SM + 1];
+  // stage s (local group index) holds scale group gb + s in buffer s % STAGES
 #pragma unroll
   for (int d = 0; d < D; ++d)
-    if (d < KG) issue_stage(d, d, sa[d]);
+    if (d < NG) issue_stage(gb + d, d);
 
-  for (int g = 0; g < KG; ++g) {
-    // stage g must have landed; the D-1 later stages may still be in flight
-    if (g + D - 1 < KG) {
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm((D - 1) * kLoadsPerStage));
+  for (int g = 0; g < NG; ++g) {
+    // stage g must have landed; the D-1 later stages may still be in flight.
+    // After the barrier every wave's share of stage g is in LDS and stage g-1
+    // (whose buffer the next issue overwrites) has been read by all waves.
+    if (g + D - 1 < NG) {
+      stage_barrier<(D - 1) * kLoadsPerStage>();
     } else {
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      stage_barrier<0>();
     }
-    __syncthreads();  // every wave's share of stage g is in LDS; stage g-1 is consumed
-    if (g + D < KG) issue_stage(g + D, (g + D) % STAGES, sa[D]);
-    const float sbC = sa[0][SM];
+    if (g + D < NG) issue_stage(gb + g + D, (g + D) % STAGES);
 
-    const uint8_t* bB = smem + (g % STAGES) * kStage;
-    const uint8_t* bA = bB + BN * 128;
+    const uint8_t* st = smem + (g % STAGES) * kStage;
+    const uint8_t* bB = st;
+    const uint8_t* bA = st + kOffA;
+    const float* sA = reinterpret_cast<const float*>(st + kOffSA);
+    const float sbC = reinterpret_cast<const float*>(st + kOffSB)[(wn * TN) >> 7];
     i32x8 aop[SM];
 #pragma unroll
     for (int j = 0; j < SM; ++j) aop[j] = lds_operand(bA, wm * TM + 16 * j + rsub, c0);
     float sab[SM];
 #pragma unroll
-    for (int j = 0; j < SM; ++j) sab[j] = sa[0][j] * sbC;
+    for (int j = 0; j < SM; ++j) sab[j] = sA[wm * TM + 16 * j + rsub] * sbC;
     // the MFMAs of weight slice i are independent of the promotion FMAs of
     // slice i-1, so the matrix core and the VALU overlap (the scheduler
     // interleaves them; the second wave on the SIMD fills the rest)
+    // (partials are live two slices at a time: fewer registers, which the
+    // 128x64 wave tile needs to stay at 256 without spilling)
+    constexpr int PJ = SM >= 4 ? 2 : SM;
 #pragma unroll
     for (int i = 0; i < SN; ++i) {
       const i32x8 bop = lds_operand(bB, wn * TN + 16 * i + rsub, c0);
-      f32x4 pv[SM];
 #pragma unroll
-      for (int j = 0; j < SM; ++j) pv[j] = mfma_group(bop, aop[j]);
+      for (int j0 = 0; j0 < SM; j0 += PJ) {
+        f32x4 pv[PJ];
 #pragma unroll
-      for (int j = 0; j < SM; ++j)
+        for (int j = 0; j < PJ; ++j) pv[j] = mfma_group(bop, aop[j0 + j]);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(pv[j][r], sab[j], acc[i][j][r]);
+        for (int j = 0; j < PJ; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            acc[i][j0 + j][r] = __builtin_fmaf(pv[j][r], sab[j0 + j], acc[i][j0 + j][r]);
+      }
     }
-#pragma unroll
-    for (int d = 0; d < D; ++d)
-#pragma unroll
-      for (int j = 0; j <= SM; ++j) sa[d][j] = sa[d + 1][j];
   }
 
+  if (split > 1) {
+    f32x4 part[SN * SM];
 #pragma unroll
-  for (int i = 0; i < SN; ++i)
+    for (int i = 0; i < SN; ++i)
 #pragma unroll
-    for (int j = 0; j < SM; ++j)
-      store_out4<OUT_DT>(a, m0 + wm * TM + 16 * j + rsub, n0 + wn * TN + 16 * i + 4 * c0,
-                         acc[i][j]);
+      for (int j = 0; j < SM; ++j) part[i * SM + j] = acc[i][j];
+    auto valid = [&](int q) { return m0 + wm * TM + 16 * (q % SM) + rsub < M; };
+    if (!splitk_fixup<SN * SM>(a, part, split, z, (int)blockIdx.x, (int64_t)gridDim.x,
+                               NW * SN * SM, wave * SN * SM, lane, valid))
+      return;
+#pragma unroll
+    for (int i = 0; i < SN; ++i)
+#pragma unroll
+      for (int j = 0; j < SM; ++j) acc[i][j] = part[i * SM + j];
+  }
+
+  if constexpr (OUT_DT == kFp32) {
+#pragma unroll
+    for (int i = 0; i < SN; ++i)
+#pragma unroll
+      for (int j = 0; j < SM; ++j)
+        store_out4<OUT_DT>(a, m0 + wm * TM + 16 * j + rsub, n0 + wn * TN + 16 * i + 4 * c0,
+                           acc[i][j]);
+  } else {
+    // 16-bit outputs leave through LDS: each lane's four consecutive outputs
+    // go to the C tile in LDS (rows padded by 8 bytes so the 16 rows of a
+    // store phase fall in different banks), then every row of the tile is
+    // written to C as contiguous 16-byte pieces.
+    using OT = typename OutT<OUT_DT>::T;
+    constexpr int kRow = BN * 2 + 8;
+    static_assert(BM * kRow <= STAGES * kStage, "C tile must fit in the stage buffers");
+    stage_barrier<0>();  // all waves are done with the stage buffers
+#pragma unroll
+    for (int i = 0; i < SN; ++i)
+#pragma unroll
+      for (int j = 0; j < SM; ++j) {
+        const int ml = wm * TM + 16 * j + rsub, nl = wn * TN + 16 * i + 4 * c0;
+        typedef OT ot4 __attribute__((ext_vector_type(4)));
+        *reinterpret_cast<ot4*>(smem + ml * kRow + nl * 2) =
+            ot4{(OT)acc[i][j][0], (OT)acc[i][j][1], (OT)acc[i][j][2], (OT)acc[i][j][3]};
+      }
+    stage_barrier<0>();
+    constexpr int kChunks = BN / 8;  // 16-byte pieces per tile row
+    OT* C = reinterpret_cast<OT*>(a.c);
+    const bool vec = a.vec_ok && (N % 8) == 0;
+    for (int idx = threadIdx.x; idx < BM * kChunks; idx += 64 * NW) {
+      const int ml = idx / kChunks, cc = idx % kChunks;
+      const int m = m0 + ml, n = n0 + cc * 8;
+      if (m >= M || n >= N) continue;
+      const uint8_t* src = smem + ml * kRow + cc * 16;
+      OT* dst = C + (int64_t)m * N + n;
+      if (vec && n + 7 < N) {
+        __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(src),
+                                    reinterpret_cast<u32x4*>(dst));
+      } else {
+        const OT* e = reinterpret_cast<const OT*>(src);
+        for (int r = 0; r < 8 && n + r < N; ++r) dst[r] = e[r];
+      }
+    }
+  }
 }
 
 // ---- kernel table -------------------------------------------------------------
@@ -414,10 +529,10 @@ struct CfgEntry {
   KernelFn fn[3];  // [out_dt index]
 };
 
-#define DECODE_CFG(NT, MT, W, U, NAME)                                                        \
-  {1, 16 * NT, 16 * MT, W, NAME,                                                               \
-   {gemm_decode_kernel<NT, MT, W, U, kFp32>, gemm_decode_kernel<NT, MT, W, U, kFp16>,          \
-    gemm_decode_kernel<NT, MT, W, U, kBf16>}}
+#define DECODE_CFG(MT, WK, U, NAME)                                                           \
+  {1, 16, 16 * MT, WK, NAME,                                                                   \
+   {gemm_decode_kernel<MT, WK, U, kFp32>, gemm_decode_kernel<MT, WK, U, kFp16>,                \
+    gemm_decode_kernel<MT, WK, U, kBf16>}}
 #define PREFILL_CFG(BN, BM, WN, WM, ST, NAME)                                                 \
   {2, BN, BM, WN * WM, NAME,                                                                   \
    {gemm_prefill_kernel<BN, BM, WN, WM, ST, kFp32>,                                            \
@@ -425,12 +540,12 @@ struct CfgEntry {
     gemm_prefill_kernel<BN, BM, WN, WM, ST, kBf16>}}
 
 const CfgEntry kCfgs[] = {
-    DECODE_CFG(1, 1, 16, 4, "dec_n16_m16_w16"),
-    DECODE_CFG(1, 1, 8, 4, "dec_n16_m16_w8"),
-    DECODE_CFG(1, 2, 16, 4, "dec_n16_m32_w16"),
-    DECODE_CFG(1, 4, 16, 2, "dec_n16_m64_w16"),
-    DECODE_CFG(2, 4, 8, 2, "dec_n32_m64_w8"),
-    DECODE_CFG(2, 1, 8, 4, "dec_n32_m16_w8"),
+    DECODE_CFG(1, 1, 8, "dec_m16_k1_u8"),
+    DECODE_CFG(1, 2, 8, "dec_m16_k2_u8"),
+    DECODE_CFG(1, 4, 8, "dec_m16_k4_u8"),
+    DECODE_CFG(1, 8, 8, "dec_m16_k8_u8"),
+    DECODE_CFG(2, 4, 4, "dec_m32_k4_u4"),
+    DECODE_CFG(4, 4, 2, "dec_m64_k4_u2"),
     PREFILL_CFG(256, 128, 4, 2, 3, "pre_n256_m128_w8_s3"),
     PREFILL_CFG(128, 256, 2, 4, 3, "pre_n128_m256_w8_s3"),
     PREFILL_CFG(128, 128, 2, 2, 2, "pre_n128_m128_w4_s2"),
@@ -556,8 +671,16 @@ extern "C" int inferop_hip_gemm_w8a8_block(void* c, const uint8_t* a_q, const fl
                        dim3(64 * cf.waves), 0, st, args);
   } else {
     const int64_t tiles = tn * tm;
-    if (tiles > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL(cf.fn[di], dim3((unsigned)tiles), dim3(64 * cf.waves), 0, st, args);
+    int split = launch->split_k < 1 ? 1 : launch->split_k;
+    if (split > kg) split = kg;
+    if (tiles > 0x7FFFFFFF || split > 65535) return hipErrorInvalidConfiguration;
+    if (split > 1) {
+      const size_t bytes = (size_t)split * (size_t)tiles * (size_t)cf.bn * (size_t)cf.bm * 4;
+      hipError_t e = get_workspace(st, bytes, (size_t)tiles, &args.ws, &args.counters);
+      if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(cf.fn[di], dim3((unsigned)tiles, (unsigned)split), dim3(64 * cf.waves), 0,
+                       st, args);
   }
   return hipGetLastError();
 }

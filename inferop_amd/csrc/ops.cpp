@@ -63,12 +63,12 @@ int status_of_hip(int e) { return e == 0 ? INFEROP_OK : INFEROP_ERR_LAUNCH; }
 // ---- gfx950 tile selection ----------------------------------------------------
 // Kernel table indices (inferop_amd/csrc/gemm.hip, kCfgs).
 enum GemmCfg : int32_t {
-  kDecN16M16W16 = 0,
-  kDecN16M16W8 = 1,
-  kDecN16M32W16 = 2,
-  kDecN16M64W16 = 3,
-  kDecN32M64W8 = 4,
-  kDecN32M16W8 = 5,
+  kDecM16K1 = 0,
+  kDecM16K2 = 1,
+  kDecM16K4 = 2,
+  kDecM16K8 = 3,
+  kDecM32K4 = 4,
+  kDecM64K4 = 5,
   kPreN256M128S3 = 6,
   kPreN128M256S3 = 7,
   kPreN128M128S2 = 8,
@@ -85,31 +85,39 @@ GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
   if (cus <= 0) cus = 256;
   const int64_t kg = k / 128;
   if (m <= 64) {
-    // HBM-bound: waves own 16 (or 32) weight rows and a few scale groups and
-    // issue all of their loads at once; the workgroup's waves split K so the
-    // weight matrix is streamed by thousands of waves in flight.  Split K
-    // across workgroups only when the N tiles alone cannot occupy the CUs.
+    // HBM-bound: a workgroup owns 16 weight rows; its WK waves split the
+    // scale groups, each streaming at most U groups with all loads in flight.
+    // K is split across workgroups only when WK * U groups do not cover it.
     int32_t cfg;
-    int64_t rows;
+    int64_t per_wg;
     if (m <= 16) {
-      cfg = kDecN16M16W16, rows = 16;
+      cfg = kDecM16K8, per_wg = 8 * 8;
     } else if (m <= 32) {
-      cfg = kDecN16M32W16, rows = 16;
+      cfg = kDecM32K4, per_wg = 4 * 4;
     } else {
-      cfg = kDecN32M64W8, rows = 32;
+      cfg = kDecM64K4, per_wg = 4 * 2;
     }
-    const int64_t tiles = (n + rows - 1) / rows;
-    int64_t split = 1;
-    if (tiles < cus) split = (cus + tiles - 1) / tiles;
-    if (split > kg / 8) split = kg / 8;
+    int64_t split = (kg + per_wg - 1) / per_wg;
     if (split < 1) split = 1;
     return {cfg, int32_t(split)};
   }
-  // MFMA-bound: 256x256 tiles when they give every CU a workgroup, else the
-  // 128x128 tile (two workgroups per CU).
+  // MFMA-bound: a 256x256 tile runs alone on a CU and does four 128x128
+  // tiles' work in about 1.5x their time (two 128x128 tiles share a CU).
+  // Count whole rounds of workgroups for both and take the cheaper one.
   const int64_t t256 = ((n + 255) / 256) * ((m + 255) / 256);
-  if (t256 >= cus) return {kPreN256M256S2, 1};
-  return {kPreN128M128S2, 1};
+  const int64_t t128 = ((n + 127) / 128) * ((m + 127) / 128);
+  const int64_t r256 = (t256 + cus - 1) / cus;
+  const int64_t r128 = (t128 + 2 * cus - 1) / (2 * cus);
+  if (2 * r256 * 3 < 2 * 2 * r128) return {kPreN256M256S2, 1};
+  // too few 128x128 tiles to fill the CUs: split K across workgroups
+  int64_t split = 1;
+  if (t128 < cus) {
+    split = (cus + t128 - 1) / t128;
+    const int64_t max_split = kg >= 16 ? kg / 8 : kg / 2;
+    if (split > max_split) split = max_split;
+    if (split < 1) split = 1;
+  }
+  return {kPreN128M128S2, int32_t(split)};
 }
 
 // ---- implementations shared by the C++ and C entry points --------------------
