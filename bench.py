@@ -54,11 +54,59 @@ def parse():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--traffic-pass", action="store_true",
+                   help="launch a 256 MiB streaming kernel and every decode-step kernel once "
+                        "each (cold weights) for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs; "
+                        "prints the launches in order with their algorithmic bytes")
     return p.parse_args()
+
+
+def traffic_pass():
+    """Counter-collection workload.  The first launch is a plain streaming
+    kernel (fp32 y = x * 1 over 256 MiB: 256 MiB read + 256 MiB written) whose
+    FETCH_SIZE / WRITE_SIZE readings calibrate the counters; then, for every
+    decode case, one quantizer and one GEMM launch, each GEMM on a weight copy
+    no earlier launch touched, so the counters see HBM reads, not cache hits."""
+    import torch
+
+    import inferop_amd as ia
+
+    ia.lib()
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    launches = []
+    n_el = 64 << 20
+    x = torch.randn(n_el, generator=gen, device=dev)
+    y = torch.empty_like(x)
+    cases = [(m, n, k) for m in DECODE_M for (n, k) in DECODE_NK]
+    ws = [(torch.randint(0, 0x7E, (n, k), generator=gen, device=dev, dtype=torch.int32)
+           .to(torch.uint8),
+           torch.rand(((n + 127) // 128, k // 128), generator=gen, device=dev) * 1e-3 + 1e-4)
+          for (_, n, k) in cases]
+    acts = [torch.randn((m, k), generator=gen, device=dev).to(torch.bfloat16)
+            for (m, _, k) in cases]
+    torch.cuda.synchronize()
+    torch.mul(x, 1.0, out=y)
+    torch.cuda.synchronize()
+    launches.append({"launch": "calibration fp32 y = x * 1", "read": 4 * n_el, "write": 4 * n_el})
+    for (m, n, k), (bq, bs), a in zip(cases, ws, acts):
+        q, s = ia.quantize(a)
+        torch.cuda.synchronize()
+        launches.append({"launch": f"quant m={m} k={k}", "read": 2 * m * k,
+                         "write": m * k + 4 * m * (k // 128)})
+        ia.gemm(q, s, bq, bs)
+        torch.cuda.synchronize()
+        cfg, split = ia.gemm_select(m, n, k)
+        launches.append({"launch": f"gemm m={m} n={n} k={k} {ia.gemm_config_name(cfg)}/s{split}",
+                         "read": gemm_bytes(m, n, k) - 2 * m * n, "write": 2 * m * n})
+    print(json.dumps({"traffic_pass": launches}), flush=True)
 
 
 def main():
     args = parse()
+    if args.traffic_pass:
+        traffic_pass()
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this benchmark runs on exactly one GPU: the FP8 path has no "
                                    "multi-GPU component here (sharding is described in "

@@ -20,15 +20,16 @@
 //
 // Two kernel families:
 //
-// * decode (M <= 64 per tile, HBM-bound): no LDS for operands and no barrier
-//   in the main loop.  Each wave streams its weight rows straight from HBM
-//   into MFMA registers (non-temporal 16-byte loads, U scale groups in flight)
-//   and re-reads the small activation tile from L2.  The waves of a workgroup
-//   split the workgroup's K range and are summed through LDS; workgroups
-//   split K further (split-K) and the last one to finish a tile adds the
-//   partials in split order (deterministic).  Partials travel through
-//   device-coherent stores and loads (sc1) and a device-scope atomic counter,
-//   so no L2 writeback or invalidate is needed.
+// * decode (M <= 64 per tile, HBM-bound): no barrier in the main loop.  Each
+//   wave streams its 16 weight rows, U scale groups at a time, with direct
+//   global->LDS loads into an LDS region only it uses (whole 128-byte rows per
+//   8 lanes, the access pattern HBM streams best), reads them back in MFMA
+//   layout, and takes the small activation tile from L2 straight into
+//   registers.  The waves of a workgroup split the workgroup's K range and are
+//   summed through LDS; workgroups split K further (split-K) and the last one
+//   to finish a tile adds the partials in split order (deterministic).
+//   Partials travel through device-coherent stores and loads and a
+//   device-scope atomic counter, so no L2 writeback or invalidate is needed.
 //
 // * prefill (large M, MFMA-bound): a BN x BM output tile per workgroup, A and
 //   B staged in LDS by direct global->LDS loads (global_load_lds_dwordx4, no
@@ -674,6 +675,8 @@ extern "C" int inferop_hip_gemm_w8a8_block(void* c, const uint8_t* a_q, const fl
     int split = launch->split_k < 1 ? 1 : launch->split_k;
     if (split > kg) split = kg;
     if (tiles > 0x7FFFFFFF || split > 65535) return hipErrorInvalidConfiguration;
+    // tile rows are addressed with 32-bit buffer offsets
+    if ((int64_t)(cf.bn > cf.bm ? cf.bn : cf.bm) * k > 0x7FFFFFFF) return hipErrorInvalidValue;
     if (split > 1) {
       const size_t bytes = (size_t)split * (size_t)tiles * (size_t)cf.bn * (size_t)cf.bm * 4;
       hipError_t e = get_workspace(st, bytes, (size_t)tiles, &args.ws, &args.counters);

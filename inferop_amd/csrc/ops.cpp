@@ -84,14 +84,20 @@ struct GemmChoice {
 GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
   if (cus <= 0) cus = 256;
   const int64_t kg = k / 128;
-  if (m <= 64) {
+  // The prefill kernels address a tile's rows with 32-bit offsets (256 rows
+  // x K bytes); a K beyond that runs on the decode kernels at any M.
+  if (m <= 64 || k * 256 > 0x7FFFFFFF) {
     // HBM-bound: a workgroup owns 16 weight rows; its WK waves split the
     // scale groups, each streaming at most U groups with all loads in flight.
     // K is split across workgroups only when WK * U groups do not cover it.
     int32_t cfg;
     int64_t per_wg;
     if (m <= 16) {
-      cfg = kDecM16K8, per_wg = 8 * 8;
+      // fewest waves whose U=8 groups each cover K: short K keeps a 16-row
+      // weight stripe in one or two waves instead of idling eight.
+      if (kg <= 16) cfg = kDecM16K2, per_wg = 2 * 8;
+      else if (kg <= 32) cfg = kDecM16K4, per_wg = 4 * 8;
+      else cfg = kDecM16K8, per_wg = 8 * 8;
     } else if (m <= 32) {
       cfg = kDecM32K4, per_wg = 4 * 4;
     } else {
@@ -109,11 +115,14 @@ GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
   const int64_t r256 = (t256 + cus - 1) / cus;
   const int64_t r128 = (t128 + 2 * cus - 1) / (2 * cus);
   if (2 * r256 * 3 < 2 * 2 * r128) return {kPreN256M256S2, 1};
-  // too few 128x128 tiles to fill the CUs: split K across workgroups
+  // too few 128x128 tiles to fill the CUs: split K across workgroups, each
+  // split keeping at least 16 scale groups (below that the fp32 partial
+  // round trip costs more than the idle CUs) and at most four splits.
   int64_t split = 1;
   if (t128 < cus) {
     split = (cus + t128 - 1) / t128;
-    const int64_t max_split = kg >= 16 ? kg / 8 : kg / 2;
+    int64_t max_split = kg / 16;
+    if (max_split > 4) max_split = 4;
     if (split > max_split) split = max_split;
     if (split < 1) split = 1;
   }
