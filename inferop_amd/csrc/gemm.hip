@@ -126,7 +126,10 @@ __device__ __forceinline__ void store_out4(const GemmArgs& a, int m, int n, cons
 // pair_base .. pair_base+LP-1 of the tile's `pairs` pairs; valid(q) says
 // whether this lane's q-th pair carries data (inside M, owned by this wave).
 // Returns true in the workgroup that arrives last for the tile; `part` then
-// holds the sum over all splits, added in split order.
+// holds the sum over all splits, added in split order.  Element r of a lane's
+// pair q sits at float (q * 4 + r) * 64 + lane of the wave's slot, so every
+// store and load instruction covers 256 contiguous bytes (these accesses
+// bypass the non-coherent caches; scattered 4-byte ones cost whole lines).
 template <int LP, typename Valid>
 __device__ __forceinline__ bool splitk_fixup(const GemmArgs& a, f32x4 (&part)[LP], int split,
                                              int z, int tile, int64_t tiles, int pairs,
@@ -139,7 +142,7 @@ __device__ __forceinline__ bool splitk_fixup(const GemmArgs& a, f32x4 (&part)[LP
     if (!valid(q)) continue;
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      __hip_atomic_store(mine + (q * 64 + lane) * 4 + r, part[q][r], __ATOMIC_RELAXED,
+      __hip_atomic_store(mine + (q * 4 + r) * 64 + lane, part[q][r], __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
   }
   __builtin_amdgcn_s_waitcnt(0);  // this wave's device-coherent stores are acknowledged
@@ -157,10 +160,10 @@ __device__ __forceinline__ bool splitk_fixup(const GemmArgs& a, f32x4 (&part)[LP
     f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int zz = 0; zz < split; ++zz) {
       const float* src = a.ws + ((int64_t)zz * tiles + tile) * tile_floats +
-                         (int64_t)pair_base * 256 + (q * 64 + lane) * 4;
+                         (int64_t)pair_base * 256 + q * 256 + lane;
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        sum[r] += __hip_atomic_load(src + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sum[r] += __hip_atomic_load(src + r * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     part[q] = sum;
   }
@@ -329,17 +332,23 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_prefill_kernel(GemmArgs a) 
   // one stage in LDS: B tile | A tile | activation scales | weight scale
   constexpr int kOffA = BN * 128;
   constexpr int kOffSA = (BN + BM) * 128;
-  constexpr int kOffSB = kOffSA + BM * 4;
+  constexpr int kSaWaves = (BM + 63) / 64;  // waves that fetch activation scales
+  constexpr int kOffSB = kOffSA + kSaWaves * 256;
   constexpr int kStage = ((kOffSB + 256) + 1023) / 1024 * 1024;
   constexpr int RB = BN / 8 / NW;  // 1 KB row blocks of B each wave loads per stage
-  constexpr int RA = BM / 8 / NW;
+  // A has BM / 8 row blocks; when there are fewer than waves, the extra waves
+  // repeat a block (same bytes to the same LDS place) so that every wave
+  // issues the same number of loads per stage, which the wait counts assume.
+  constexpr int kABlocks = BM / 8;
+  constexpr int RA = (kABlocks + NW - 1) / NW;
   constexpr int kLoadsPerStage = RB + RA + 1;  // + one scale load per wave
   constexpr int D = STAGES - 1;                // prefetch distance in scale groups
   static_assert(STAGES >= 2 && STAGES <= 4, "2 to 4 LDS stages");
   static_assert(TN % 16 == 0 && TM % 16 == 0, "wave tile must be a multiple of 16");
   static_assert(128 % TN == 0, "a wave must stay inside one 128-row weight block");
-  static_assert(BN % (8 * NW) == 0 && BM % (8 * NW) == 0, "row blocks must split evenly");
-  static_assert(BM % 64 == 0 && BM / 64 < NW, "activation scales take BM/64 waves, sb one more");
+  static_assert(BN >= 128 ? BN % 128 == 0 : 128 % BN == 0, "tiles align to weight blocks");
+  static_assert(BN % (8 * NW) == 0, "B row blocks must split evenly over the waves");
+  static_assert((BM < 64 || BM % 64 == 0) && kSaWaves < NW, "scale loads need a spare wave");
 
   __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * kStage];
 
@@ -370,19 +379,20 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_prefill_kernel(GemmArgs a) 
   const int lrow = lane >> 3;
   const int loff = lrow * K + ((lane & 7) ^ lrow) * 16;
   const int rsub = lane & 15, c0 = lane >> 4;
-  // scale loads: waves 0 .. BM/64-1 fetch 64 activation scales each (one per
-  // lane, row wave*64 + lane), the other waves fetch the weight scale of the
+  // scale loads: waves 0 .. kSaWaves-1 fetch 64 activation scales each (one
+  // per lane, row wave*64 + lane), the other waves fetch the weight scale of the
   // tile's first 128-row block (every wave of the tile shares it when BN <=
   // 128; otherwise each wave reads its own block's scale, see below)
-  const bool sa_wave = wave < BM / 64;
+  const bool sa_wave = wave < kSaWaves;
   const float* scale_src;
   int scale_dst;
   if (sa_wave) {
     scale_src = a.as + (int64_t)(m0 + min(wave * 64 + lane, mlast)) * KG;
     scale_dst = kOffSA + wave * 256;
   } else {
-    // lanes 0..BN/128-1 fetch the weight scales of the tile's blocks
-    const int nb = min((n0 >> 7) + min(lane, BN / 128 - 1), NB - 1);
+    // lanes 0..kSbBlocks-1 fetch the weight scales of the tile's blocks
+    constexpr int kSbBlocks = BN >= 128 ? BN / 128 : 1;  // weight blocks the tile spans
+    const int nb = min((n0 >> 7) + min(lane, kSbBlocks - 1), NB - 1);
     scale_src = a.bs + (int64_t)nb * KG;
     scale_dst = kOffSB;
   }
@@ -396,9 +406,10 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_prefill_kernel(GemmArgs a) 
     for (int r = 0; r < RB; ++r)
       buffer_to_lds16(rB, sb + 8 * (wave + r * NW) * 128, loff, 8 * (wave + r * NW) * K + g * 128);
 #pragma unroll
-    for (int r = 0; r < RA; ++r)
-      buffer_to_lds16(rA, sb + kOffA + 8 * (wave + r * NW) * 128, loff,
-                      8 * (wave + r * NW) * K + g * 128);
+    for (int r = 0; r < RA; ++r) {
+      const int blk = (wave + r * NW) % kABlocks;
+      buffer_to_lds16(rA, sb + kOffA + 8 * blk * 128, loff, 8 * blk * K + g * 128);
+    }
   };
 
   f32x4 acc[SN][SM];
@@ -552,6 +563,11 @@ const CfgEntry kCfgs[] = {
     PREFILL_CFG(128, 128, 2, 2, 2, "pre_n128_m128_w4_s2"),
     PREFILL_CFG(128, 128, 2, 2, 4, "pre_n128_m128_w4_s4"),
     PREFILL_CFG(256, 256, 2, 4, 2, "pre_n256_m256_w8_s2"),
+    PREFILL_CFG(128, 64, 8, 1, 4, "pre_n128_m64_w8_s4"),
+    PREFILL_CFG(128, 32, 8, 1, 4, "pre_n128_m32_w8_s4"),
+    PREFILL_CFG(128, 16, 8, 1, 4, "pre_n128_m16_w8_s4"),
+    PREFILL_CFG(64, 64, 4, 1, 4, "pre_n64_m64_w4_s4"),
+    PREFILL_CFG(128, 64, 8, 1, 3, "pre_n128_m64_w8_s3"),
 };
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 

@@ -74,6 +74,11 @@ enum GemmCfg : int32_t {
   kPreN128M128S2 = 8,
   kPreN128M128S4 = 9,
   kPreN256M256S2 = 10,
+  kPreN128M64S4 = 11,
+  kPreN128M32S4 = 12,
+  kPreN128M16S4 = 13,
+  kPreN64M64S4 = 14,
+  kPreN128M64S3 = 15,
 };
 
 struct GemmChoice {
@@ -86,7 +91,30 @@ GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
   const int64_t kg = k / 128;
   // The prefill kernels address a tile's rows with 32-bit offsets (256 rows
   // x K bytes); a K beyond that runs on the decode kernels at any M.
-  if (m <= 64 || k * 256 > 0x7FFFFFFF) {
+  const bool huge_k = k * 256 > 0x7FFFFFFF;
+  // K split for the LDS-staged small tiles: as many splits as keep every
+  // workgroup resident at two per CU (a second partial round costs more than
+  // the splits gain), each split keeping at least four scale groups.
+  auto small_tile_split = [&](int64_t tiles) {
+    int64_t split = 2 * cus / tiles;
+    if (split > kg / 4) split = kg / 4;
+    return split < 1 ? int64_t(1) : split;
+  };
+  if (m > 16 && m <= 64 && !huge_k) {
+    // HBM-bound, but the activation tile is too tall to re-read from L2 per
+    // 16 weight rows: 128 weight rows x 16 activation rows per workgroup with
+    // A and B staged through LDS; the M tiles of one N tile run back to back
+    // on one XCD and share B in its L2.
+    const int64_t tiles = ((n + 127) / 128) * ((m + 15) / 16);
+    return {kPreN128M16S4, int32_t(small_tile_split(tiles))};
+  }
+  if (m > 64 && m <= 128 && !huge_k && ((n + 127) / 128) * ((m + 127) / 128) < cus) {
+    // Still HBM-bound and too few 128x128 tiles to occupy every CU: 64x64
+    // tiles with four LDS stages keep more weight bytes in flight per CU.
+    const int64_t tiles = ((n + 63) / 64) * ((m + 63) / 64);
+    return {kPreN64M64S4, int32_t(small_tile_split(tiles))};
+  }
+  if (m <= 64 || huge_k) {
     // HBM-bound: a workgroup owns 16 weight rows; its WK waves split the
     // scale groups, each streaming at most U groups with all loads in flight.
     // K is split across workgroups only when WK * U groups do not cover it.

@@ -147,7 +147,8 @@ def test_gemm_selection_covers_configs():
             cfg, split = inferop_amd.gemm_select(m, n, k)
             assert 0 <= cfg < n_cfg
             assert 1 <= split <= k // 128
-    assert inferop_amd.gemm_select(1, 4096, 7168)[1] > 1
+    # a K longer than one workgroup's waves cover is split across workgroups
+    assert inferop_amd.gemm_select(1, 4096, 8 * 7168)[1] > 1
 
 
 @pytest.mark.skipif(shutil.which("nm") is None, reason="binutils missing")
