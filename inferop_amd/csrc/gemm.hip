@@ -286,6 +286,100 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_kernel(GemmArgs a) {
   }
 }
 
+// ---- decode kernel with LDS-staged activations ------------------------------------
+// grid: x = N tiles of 16 rows, y = K splits, z = M tiles of 16 rows.
+// As gemm_decode_kernel<1, ...>, but the activation slice of every scale group
+// also arrives by direct-to-LDS loads (8 lanes per 128-byte row segment, the
+// pattern the weights use) instead of 16-byte register loads that touch half
+// lines, and the U groups of a batch are consumed in the order they land.
+// Each slot is its own LDS variable, so the compiler waits for exactly the
+// loads of the slot being read rather than for the whole batch.
+template <int WK, int U, int OUT_DT>
+__global__ __launch_bounds__(64 * WK) void gemm_decode_lds_kernel(GemmArgs a) {
+  static_assert(U >= 1 && U <= 4, "1 to 4 slots per wave");
+  constexpr int kSlot = WK * 4096;  // per wave: 16 weight rows + 16 activation rows
+  __shared__ __attribute__((aligned(1024))) uint8_t slot0[kSlot];
+  __shared__ __attribute__((aligned(1024))) uint8_t slot1[U > 1 ? kSlot : 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t slot2[U > 2 ? kSlot : 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t slot3[U > 3 ? kSlot : 16];
+  auto slot = [&](int u) -> uint8_t* {
+    return u == 0 ? slot0 : u == 1 ? slot1 : u == 2 ? slot2 : slot3;
+  };
+  const int lane = threadIdx.x & 63;
+  const int wk = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int M = a.m, N = a.n, K = a.k;
+  const int KG = K >> 7;
+  const int NB = (N + 127) >> 7;
+  const int n0 = blockIdx.x * 16;
+  const int m0 = blockIdx.z * 16;
+  const int split = gridDim.y, z = blockIdx.y;
+  const int gz0 = (int)((int64_t)z * KG / split), gz1 = (int)((int64_t)(z + 1) * KG / split);
+  const int cnt = gz1 - gz0;
+  const int gw0 = gz0 + wk * cnt / WK, gw1 = gz0 + (wk + 1) * cnt / WK;
+  const int rsub = lane & 15, c0 = lane >> 4;
+  // DMA slots: instruction h covers rows 8h .. 8h+7; lane -> row 8h + (lane >> 3),
+  // chunk (lane & 7) ^ (lane >> 3).  Rows past the end read as zeros.
+  const int lrow = lane >> 3;
+  const int lcol = ((lane & 7) ^ lrow) * 16;
+  const __amdgpu_buffer_rsrc_t rB = make_rsrc(a.bq + (int64_t)n0 * K, (uint32_t)(min(16, N - n0) * K));
+  const __amdgpu_buffer_rsrc_t rA = make_rsrc(a.aq + (int64_t)m0 * K, (uint32_t)(min(16, M - m0) * K));
+  const int off0 = lrow * K + lcol, off1 = (8 + lrow) * K + lcol;
+  const float* sbp = a.bs + (int64_t)min(n0 >> 7, NB - 1) * KG;
+  const float* sap = a.as + (int64_t)min(m0 + rsub, M - 1) * KG;
+  const int wo = wk * 4096;  // this wave's part of every slot
+
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int g = gw0; g < gw1; g += U) {
+    // scales first, then the slots in the order they are consumed
+    float sav[U], sbv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int gg = min(g + u, gw1 - 1);
+      sav[u] = sap[gg];
+      sbv[u] = sbp[gg];
+    }
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int gg = min(g + u, gw1 - 1);
+      uint8_t* sl = slot(u) + wo;
+      buffer_to_lds16(rB, sl, off0, gg * 128);
+      buffer_to_lds16(rB, sl + 1024, off1, gg * 128);
+      buffer_to_lds16(rA, sl + 2048, off0, gg * 128);
+      buffer_to_lds16(rA, sl + 3072, off1, gg * 128);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (g + u < gw1) {
+        const uint8_t* sl = slot(u) + wo;
+        const f32x4 pv = mfma_group(lds_operand(sl, rsub, c0), lds_operand(sl + 2048, rsub, c0));
+        const float sc = sav[u] * sbv[u];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] = __builtin_fmaf(pv[r], sc, acc[r]);
+      }
+    }
+  }
+
+  // sum the WK slices through LDS: wave 0 ends up with the tile
+  if constexpr (WK > 1) {
+    __shared__ f32x4 red[WK - 1][64];
+    if (wk > 0) red[wk - 1][lane] = acc;
+    __syncthreads();
+    if (wk == 0) {
+#pragma unroll
+      for (int w = 0; w < WK - 1; ++w) acc += red[w][lane];
+    }
+  }
+  f32x4 part[1] = {acc};
+  if (split > 1) {
+    const int tile = blockIdx.z * gridDim.x + blockIdx.x;
+    const int64_t tiles = (int64_t)gridDim.x * gridDim.z;
+    auto valid = [&](int) { return wk == 0 && m0 + rsub < M; };
+    if (!splitk_fixup<1>(a, part, split, z, tile, tiles, 1, 0, lane, valid)) return;
+  }
+  if (wk == 0) store_out4<OUT_DT>(a, m0 + rsub, n0 + 4 * c0, part[0]);
+}
+
 // ---- prefill kernel --------------------------------------------------------------
 // 1-D grid over output tiles; waves arranged WN (along N) x WM (along M).
 __device__ __forceinline__ void tile_of(int bid, int nblk, int tiles_n, int tiles_m, int* tn,
@@ -350,7 +444,17 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_prefill_kernel(GemmArgs a) 
   static_assert(BN % (8 * NW) == 0, "B row blocks must split evenly over the waves");
   static_assert((BM < 64 || BM % 64 == 0) && kSaWaves < NW, "scale loads need a spare wave");
 
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * kStage];
+  // One LDS variable per stage: the compiler then knows that reading stage g
+  // does not touch the buffers whose direct-to-LDS loads are still in flight,
+  // and does not wait for those loads before the reads (with one array
+  // indexed by g % STAGES it must assume they alias and drain every load).
+  __shared__ __attribute__((aligned(1024))) uint8_t smem0[kStage];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem1[kStage];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem2[STAGES > 2 ? kStage : 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem3[STAGES > 3 ? kStage : 16];
+  auto stage_buf = [&](int s) -> uint8_t* {
+    return s == 0 ? smem0 : s == 1 ? smem1 : s == 2 ? smem2 : smem3;
+  };
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -397,8 +501,7 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_prefill_kernel(GemmArgs a) 
     scale_dst = kOffSB;
   }
 
-  auto issue_stage = [&](int g, int buf) {
-    uint8_t* sb = smem + buf * kStage;
+  auto issue_stage = [&](int g, uint8_t* sb) {
     __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(scale_src + g),
                                      (__attribute__((address_space(3))) void*)(sb + scale_dst), 4,
                                      0, 0);
@@ -418,12 +521,17 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_prefill_kernel(GemmArgs a) 
 #pragma unroll
     for (int j = 0; j < SM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // stage s (local group index) holds scale group gb + s in buffer s % STAGES
+  // local group g (scale group gb + g) lives in stage buffer g % STAGES
 #pragma unroll
   for (int d = 0; d < D; ++d)
-    if (d < NG) issue_stage(gb + d, d);
+    if (d < NG) issue_stage(gb + d, stage_buf(d));
 
-  for (int g = 0; g < NG; ++g) {
+  // the loop is unrolled by STAGES so every buffer index is a constant
+  for (int g0 = 0; g0 < NG; g0 += STAGES) {
+#pragma unroll
+    for (int s = 0; s < STAGES; ++s) {
+    const int g = g0 + s;
+    if (g >= NG) break;
     // stage g must have landed; the D-1 later stages may still be in flight.
     // After the barrier every wave's share of stage g is in LDS and stage g-1
     // (whose buffer the next issue overwrites) has been read by all waves.
@@ -432,9 +540,9 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_prefill_kernel(GemmArgs a) 
     } else {
       stage_barrier<0>();
     }
-    if (g + D < NG) issue_stage(gb + g + D, (g + D) % STAGES);
+    if (g + D < NG) issue_stage(gb + g + D, stage_buf((s + D) % STAGES));
 
-    const uint8_t* st = smem + (g % STAGES) * kStage;
+    const uint8_t* st = stage_buf(s);
     const uint8_t* bB = st;
     const uint8_t* bA = st + kOffA;
     const float* sA = reinterpret_cast<const float*>(st + kOffSA);
@@ -465,6 +573,7 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_prefill_kernel(GemmArgs a) 
           for (int r = 0; r < 4; ++r)
             acc[i][j0 + j][r] = __builtin_fmaf(pv[j][r], sab[j0 + j], acc[i][j0 + j][r]);
       }
+    }
     }
   }
 
@@ -498,7 +607,12 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_prefill_kernel(GemmArgs a) 
     // written to C as contiguous 16-byte pieces.
     using OT = typename OutT<OUT_DT>::T;
     constexpr int kRow = BN * 2 + 8;
-    static_assert(BM * kRow <= STAGES * kStage, "C tile must fit in the stage buffers");
+    constexpr int kRowsPerBuf = kStage / kRow;  // C-tile rows in one stage buffer
+    static_assert(STAGES * kRowsPerBuf >= BM, "C tile must fit in the stage buffers");
+    auto crow = [&](int ml) -> uint8_t* {
+      const int b = ml / kRowsPerBuf;
+      return stage_buf(b) + (ml - b * kRowsPerBuf) * kRow;
+    };
     stage_barrier<0>();  // all waves are done with the stage buffers
 #pragma unroll
     for (int i = 0; i < SN; ++i)
@@ -506,7 +620,7 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_prefill_kernel(GemmArgs a) 
       for (int j = 0; j < SM; ++j) {
         const int ml = wm * TM + 16 * j + rsub, nl = wn * TN + 16 * i + 4 * c0;
         typedef OT ot4 __attribute__((ext_vector_type(4)));
-        *reinterpret_cast<ot4*>(smem + ml * kRow + nl * 2) =
+        *reinterpret_cast<ot4*>(crow(ml) + nl * 2) =
             ot4{(OT)acc[i][j][0], (OT)acc[i][j][1], (OT)acc[i][j][2], (OT)acc[i][j][3]};
       }
     stage_barrier<0>();
@@ -517,7 +631,7 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_prefill_kernel(GemmArgs a) 
       const int ml = idx / kChunks, cc = idx % kChunks;
       const int m = m0 + ml, n = n0 + cc * 8;
       if (m >= M || n >= N) continue;
-      const uint8_t* src = smem + ml * kRow + cc * 16;
+      const uint8_t* src = crow(ml) + cc * 16;
       OT* dst = C + (int64_t)m * N + n;
       if (vec && n + 7 < N) {
         __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(src),
@@ -545,6 +659,10 @@ struct CfgEntry {
   {1, 16, 16 * MT, WK, NAME,                                                                   \
    {gemm_decode_kernel<MT, WK, U, kFp32>, gemm_decode_kernel<MT, WK, U, kFp16>,                \
     gemm_decode_kernel<MT, WK, U, kBf16>}}
+#define DECODE_LDS_CFG(WK, U, NAME)                                                            \
+  {1, 16, 16, WK, NAME,                                                                        \
+   {gemm_decode_lds_kernel<WK, U, kFp32>, gemm_decode_lds_kernel<WK, U, kFp16>,                \
+    gemm_decode_lds_kernel<WK, U, kBf16>}}
 #define PREFILL_CFG(BN, BM, WN, WM, ST, NAME)                                                 \
   {2, BN, BM, WN * WM, NAME,                                                                   \
    {gemm_prefill_kernel<BN, BM, WN, WM, ST, kFp32>,                                            \
@@ -568,6 +686,9 @@ const CfgEntry kCfgs[] = {
     PREFILL_CFG(128, 16, 8, 1, 4, "pre_n128_m16_w8_s4"),
     PREFILL_CFG(64, 64, 4, 1, 4, "pre_n64_m64_w4_s4"),
     PREFILL_CFG(128, 64, 8, 1, 3, "pre_n128_m64_w8_s3"),
+    DECODE_LDS_CFG(2, 4, "decl_k2_u4"),
+    DECODE_LDS_CFG(4, 4, "decl_k4_u4"),
+    DECODE_LDS_CFG(8, 4, "decl_k8_u4"),
 };
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
@@ -675,6 +796,8 @@ extern "C" int inferop_hip_gemm_w8a8_block(void* c, const uint8_t* a_q, const fl
   GemmArgs args{c,       a_q,    a_scales, b_q,    b_scales, nullptr,
                 nullptr, (int)m, (int)n,   (int)k, vec_ok};
   if (cf.kind == 1) {
+    // a stripe's 16 rows are addressed with 32-bit offsets
+    if (16 * k > 0x7FFFFFFF) return hipErrorInvalidValue;
     int split = launch->split_k < 1 ? 1 : launch->split_k;
     if (split > kg) split = kg;
     if (tn > 0x7FFFFFFF || split > 65535 || tm > 65535) return hipErrorInvalidConfiguration;

@@ -79,6 +79,9 @@ enum GemmCfg : int32_t {
   kPreN128M16S4 = 13,
   kPreN64M64S4 = 14,
   kPreN128M64S3 = 15,
+  kDecLdsK2 = 16,
+  kDecLdsK4 = 17,
+  kDecLdsK8 = 18,
 };
 
 struct GemmChoice {
@@ -114,19 +117,25 @@ GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
     const int64_t tiles = ((n + 63) / 64) * ((m + 63) / 64);
     return {kPreN64M64S4, int32_t(small_tile_split(tiles))};
   }
+  if (m <= 16 && !huge_k) {
+    // HBM-bound: a workgroup owns 16 weight rows and streams them, with the
+    // 16 activation rows, through per-wave LDS slots; its waves split K.
+    // Short K keeps a stripe in four waves, longer K in eight; K is split
+    // across workgroups only when the stripes alone leave CUs idle.
+    const int64_t stripes = (n + 15) / 16;
+    const int32_t cfg = kg <= 16 ? kDecLdsK4 : kDecLdsK8;
+    int64_t split = stripes < cus ? cus / stripes : 1;
+    if (split > kg / 32) split = kg / 32;
+    if (split < 1) split = 1;
+    return {cfg, int32_t(split)};
+  }
   if (m <= 64 || huge_k) {
     // HBM-bound: a workgroup owns 16 weight rows; its WK waves split the
     // scale groups, each streaming at most U groups with all loads in flight.
     // K is split across workgroups only when WK * U groups do not cover it.
     int32_t cfg;
     int64_t per_wg;
-    if (m <= 16) {
-      // fewest waves whose U=8 groups each cover K: short K keeps a 16-row
-      // weight stripe in one or two waves instead of idling eight.
-      if (kg <= 16) cfg = kDecM16K2, per_wg = 2 * 8;
-      else if (kg <= 32) cfg = kDecM16K4, per_wg = 4 * 8;
-      else cfg = kDecM16K8, per_wg = 8 * 8;
-    } else if (m <= 32) {
+    if (m <= 32) {
       cfg = kDecM32K4, per_wg = 4 * 4;
     } else {
       cfg = kDecM64K4, per_wg = 4 * 2;

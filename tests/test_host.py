@@ -147,8 +147,9 @@ def test_gemm_selection_covers_configs():
             cfg, split = inferop_amd.gemm_select(m, n, k)
             assert 0 <= cfg < n_cfg
             assert 1 <= split <= k // 128
-    # a K longer than one workgroup's waves cover is split across workgroups
-    assert inferop_amd.gemm_select(1, 4096, 8 * 7168)[1] > 1
+    # a long K over too few weight stripes to occupy every CU is split
+    assert inferop_amd.gemm_select(1, 512, 8 * 7168)[1] > 1
+    assert inferop_amd.gemm_select(1, 4096, 7168)[1] == 1
 
 
 @pytest.mark.skipif(shutil.which("nm") is None, reason="binutils missing")
