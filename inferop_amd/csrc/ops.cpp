@@ -103,13 +103,16 @@ GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
     if (split > kg / 4) split = kg / 4;
     return split < 1 ? int64_t(1) : split;
   };
-  if (m > 16 && m <= 64 && !huge_k) {
+  if (m > 32 && m <= 64 && !huge_k) {
     // HBM-bound, but the activation tile is too tall to re-read from L2 per
-    // 16 weight rows: 128 weight rows x 16 activation rows per workgroup with
-    // A and B staged through LDS; the M tiles of one N tile run back to back
-    // on one XCD and share B in its L2.
-    const int64_t tiles = ((n + 127) / 128) * ((m + 15) / 16);
-    return {kPreN128M16S4, int32_t(small_tile_split(tiles))};
+    // 16 weight rows: 128 weight rows x 32 activation rows per workgroup with
+    // A and B staged through LDS; the two M tiles of one N tile run back to
+    // back on one XCD and share B in its L2.  One workgroup fits a CU, so K
+    // is split up to one workgroup per CU.
+    const int64_t tiles = ((n + 127) / 128) * ((m + 31) / 32);
+    int64_t split = cus / tiles;
+    if (split > kg / 4) split = kg / 4;
+    return {kPreN128M32S4, int32_t(split < 1 ? 1 : split)};
   }
   if (m > 64 && m <= 128 && !huge_k && ((n + 127) / 128) * ((m + 127) / 128) < cus) {
     // Still HBM-bound and too few 128x128 tiles to occupy every CU: 64x64
@@ -117,13 +120,15 @@ GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
     const int64_t tiles = ((n + 63) / 64) * ((m + 63) / 64);
     return {kPreN64M64S4, int32_t(small_tile_split(tiles))};
   }
-  if (m <= 16 && !huge_k) {
+  if (m <= 32 && !huge_k) {
     // HBM-bound: a workgroup owns 16 weight rows and streams them, with the
     // 16 activation rows, through per-wave LDS slots; its waves split K.
     // Short K keeps a stripe in four waves, longer K in eight; K is split
     // across workgroups only when the stripes alone leave CUs idle.
+    // (17 <= M <= 32 runs two M tiles over the same weight stripe, in two
+    // waves per stripe, which leaves room for twice the workgroups.)
     const int64_t stripes = (n + 15) / 16;
-    const int32_t cfg = kg <= 16 ? kDecLdsK4 : kDecLdsK8;
+    const int32_t cfg = m > 16 ? kDecLdsK2 : kg <= 16 ? kDecLdsK4 : kDecLdsK8;
     int64_t split = stripes < cus ? cus / stripes : 1;
     if (split > kg / 32) split = kg / 32;
     if (split < 1) split = 1;
