@@ -381,13 +381,18 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_lds_kernel(GemmArgs a) {
 }
 
 // ---- prefill kernel --------------------------------------------------------------
-// 1-D grid over output tiles; waves arranged WN (along N) x WM (along M).
-__device__ __forceinline__ void tile_of(int bid, int nblk, int tiles_n, int tiles_m, int* tn,
-                                        int* tm) {
-  // The hardware deals workgroups to the 8 XCDs round-robin; renumber so each
-  // XCD owns a contiguous range of tile ids.
-  int id = bid;
-  if ((nblk & 7) == 0) id = (bid & 7) * (nblk >> 3) + (bid >> 3);
+// grid (tiles, K splits); waves arranged WN (along N) x WM (along M).
+
+// The hardware deals workgroups to the 8 XCDs round-robin in linear launch
+// order.  Renumber linear id b of nblk so that each XCD owns a contiguous
+// range of logical ids (a bijection on [0, nblk) for any nblk): XCD x holds
+// nblk / 8 ids, plus one when x < nblk % 8.
+__device__ __forceinline__ int xcd_contiguous(int b, int nblk) {
+  const int q = nblk >> 3, r = nblk & 7, x = b & 7;
+  return x * q + min(x, r) + (b >> 3);
+}
+
+__device__ __forceinline__ void tile_of(int id, int tiles_n, int tiles_m, int* tn, int* tm) {
   // Groups of GM tile-rows along M walk across all N tiles: the A rows of a
   // group and the B rows of the current column stay hot in L2.
   constexpr int GM = 8;
@@ -463,11 +468,15 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_prefill_kernel(GemmArgs a) 
   const int KG = K >> 7;
   const int NB = (N + 127) >> 7;
   const int tiles_n = (N + BN - 1) / BN, tiles_m = (M + BM - 1) / BM;
+  // logical (tile, split) of this workgroup: consecutive tiles of one split
+  // share an XCD, so the tiles reading the same A rows or B rows meet in its L2
+  const int L = xcd_contiguous((int)(blockIdx.y * gridDim.x + blockIdx.x), (int)(gridDim.x * gridDim.y));
+  const int tile = L % (int)gridDim.x;
   int tn, tm;
-  tile_of(blockIdx.x, gridDim.x, tiles_n, tiles_m, &tn, &tm);
+  tile_of(tile, tiles_n, tiles_m, &tn, &tm);
   const int n0 = tn * BN, m0 = tm * BM;
-  // split-K: blockIdx.y selects a contiguous range of scale groups
-  const int split = gridDim.y, z = blockIdx.y;
+  // split-K: split z covers a contiguous range of scale groups
+  const int split = gridDim.y, z = L / (int)gridDim.x;
   const int gb = (int)((int64_t)z * KG / split), ge = (int)((int64_t)(z + 1) * KG / split);
   const int NG = ge - gb;
   // tile buffers: rows past the last row of A or B read as zeros
@@ -584,7 +593,7 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_prefill_kernel(GemmArgs a) 
 #pragma unroll
       for (int j = 0; j < SM; ++j) part[i * SM + j] = acc[i][j];
     auto valid = [&](int q) { return m0 + wm * TM + 16 * (q % SM) + rsub < M; };
-    if (!splitk_fixup<SN * SM>(a, part, split, z, (int)blockIdx.x, (int64_t)gridDim.x,
+    if (!splitk_fixup<SN * SM>(a, part, split, z, tile, (int64_t)gridDim.x,
                                NW * SN * SM, wave * SN * SM, lane, valid))
       return;
 #pragma unroll
