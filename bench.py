@@ -37,6 +37,11 @@ DECODE_NK = ((7168, 2048), (4096, 7168), (2112, 7168))
 PREFILL_NK = ((24576, 1536), (32768, 512), (7168, 16384), (4608, 7168))
 QUANT_SHAPES = ((4096, 7168), (4096, 16384), (8192, 18432))
 PER_KERNEL_LAUNCHES = 20
+# HBM bytes per decode-GEMM launch, mean over the 9 decode shapes: FETCH_SIZE +
+# WRITE_SIZE from rocprofv3 runs of `bench.py --traffic-pass`, each scaled by
+# what the counter reads for a 256 MiB streaming kernel in the same process
+# (per-launch table and commands: profiles/decode_step_hbm_traffic.md).
+DECODE_GEMM_TRAFFIC_BYTES = 25395177
 
 
 def quant_bytes(m, k, in_bytes=2):
@@ -233,7 +238,9 @@ def main():
                        "ms_per_step_eager_launch": round(ms_step_eager, 5)},
             "roofline": {"bound": "hbm", "kernel": "w8a8 block-FP8 GEMM, decode tiles",
                          "achieved": round(gemm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(gemm_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                         "frac": round(gemm_gbs / HBM_PEAK_GBS, 4),
+                         "traffic": DECODE_GEMM_TRAFFIC_BYTES,
+                         "algorithmic_bytes_per_launch": int(g_bytes / len(cases)),
                          "algorithmic_bytes_per_step": int(g_bytes),
                          "avg_launch_us": round(g_ms / len(cases) * 1e3, 3)},
             "decode_detail": detail,
@@ -300,6 +307,32 @@ def main():
             qres.append({"m": mq, "k": kq, "us": round(us, 2), "gbs": round(gbs, 1),
                          "frac": round(gbs / HBM_PEAK_GBS, 4)})
             del xs, q, s, gq
+        # ---------------- weight block quantizer (weight-load time) ----------------
+        wres = []
+        for (nw, kw, wdt) in ((7168, 16384, torch.float32), (36864, 7168, torch.bfloat16)):
+            ebytes = 4 if wdt == torch.float32 else 2
+            nbuf = max(2, -(-(1 << 30) // (nw * kw * ebytes)))
+            ws_ = [torch.randn((nw, kw), generator=gen, device=dev).to(wdt) * 0.02
+                   for _ in range(nbuf)]
+            wq = torch.empty((nw, kw), dtype=torch.uint8, device=dev)
+            wsc = torch.empty(((nw + 127) // 128, kw // 128), dtype=torch.float32, device=dev)
+            code = DT.fp32 if wdt == torch.float32 else DT.bf16
+
+            def fw(i, ws_=ws_, wq=wq, wsc=wsc, nw=nw, kw=kw, code=code):
+                st = ia.quant_fp8_weight_block(wq, wsc, ws_[i % len(ws_)], code, nw, kw, 128, 128,
+                                               sp)
+                assert st == 0, st
+
+            gw = capture(lambda: [fw(i) for i in range(nbuf)])
+            time_graphs([gw], 2)
+            us = time_graphs([gw], 5) / nbuf * 1e3
+            wb = nw * kw * (ebytes + 1) + 4 * ((nw + 127) // 128) * (kw // 128)
+            wres.append({"n": nw, "k": kw, "dtype": str(wdt).replace("torch.", ""),
+                         "us": round(us, 2), "gbs": round(wb / (us * 1e-6) / 1e9, 1),
+                         "frac": round(wb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+            del ws_, wq, wsc, gw
+        result["weight_quant"] = {"shapes": wres, "peak_gbs": HBM_PEAK_GBS}
+
         result["quant"] = {"shapes": qres, "peak_gbs": HBM_PEAK_GBS,
                            "roofline": {"bound": "hbm", "kernel": "per-token-group quantizer",
                                         "achieved": qres[-1]["gbs"], "peak": HBM_PEAK_GBS,

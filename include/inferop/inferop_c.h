@@ -60,6 +60,15 @@ int inferop_w8a8_block_fp8_gemm(void* c, const void* a_q, const void* a_scales, 
                                 int32_t group_size, int32_t block_n, int32_t out_dt,
                                 void* stream);
 
+/* --- extension: 128x128 weight block quantizer (no counterpart in the
+ * reference ops.h; the recipe of its tests/test_gemm.cpp:28-45), see
+ * inferop::quant_fp8_weight_block in ops.h.  group_size != 128,
+ * block_n != 128, n <= 0, k <= 0 or k % 128 != 0 return INFEROP_ERR_SHAPE;
+ * dt outside {fp32, fp16, bf16} INFEROP_ERR_DTYPE; w not 16-byte or b_q not
+ * 8-byte aligned INFEROP_ERR_ARGUMENT; nothing is written in those cases. */
+int inferop_quant_fp8_weight_block(void* b_q, void* b_scales, const void* w, int32_t dt, int64_t n,
+                                   int64_t k, int32_t group_size, int32_t block_n, void* stream);
+
 /* --- tuning and testing (no counterpart in the reference) ---
  * The GEMM with an explicit kernel configuration and split-K factor instead
  * of the automatic gfx950 choice.  config in [0, inferop_gemm_num_configs()). */

@@ -1,10 +1,11 @@
 // inferop (MI355X build) : public host API for the blockwise-FP8 W8A8 path.
 //
-// Drop-in for the reference header include/inferop/ops.h.  Every declaration
-// below has the reference's exact C++ signature and default arguments, so the
+// Drop-in for the reference header include/inferop/ops.h.  Every reference
+// function below has the reference's exact C++ signature and default arguments, so the
 // Itanium-mangled symbols exported by libinferop.so are the ones a program
 // built against the reference links to.  Only the FP8 path is provided
-// (quantizer, dequantizer, blockwise GEMM) plus device introspection.
+// (quantizer, dequantizer, blockwise GEMM) plus device introspection, and one
+// extension the reference keeps in its tests: the weight block quantizer.
 //
 // All tensors are caller-owned device pointers.  `stream` is an opaque
 // hipStream_t; nullptr is the null stream.  Calls are asynchronous on that
@@ -56,5 +57,21 @@ void w8a8_block_fp8_gemm(void* c, const void* a_q, const void* a_scales, const v
                          const void* b_scales, int64_t m, int64_t n, int64_t k,
                          int group_size = 128, int block_n = 128, dtype out_dt = dtype::bf16,
                          void* stream = nullptr);
+
+// --- extension: 128x128 weight block quantization ----------------------------
+// No counterpart in the reference ops.h: the reference quantizes weights in
+// its GEMM tests (tests/test_gemm.cpp:28-45); this is that recipe on the GPU,
+// producing exactly the B_q / sb the GEMM above consumes.
+//   w:        [n, k] in dt (fp32 / fp16 / bf16), 16-byte aligned
+//   b_q:      [n, k] uint8 (E4M3), 8-byte aligned
+//   b_scales: [ceil(n/128), k/128] fp32
+//   absmax = max |w| over the block (NaN ignored)
+//   scale  = absmax == 0 ? 1 : absmax * fl32(1/448)
+//   b_q    = e4m3_rn_sat(w * fl32(1 / scale))   (product with the reciprocal)
+// Requires group_size == block_n == 128 and k % 128 == 0; other shapes,
+// dtypes and misaligned pointers are silent no-ops.
+void quant_fp8_weight_block(void* b_q, void* b_scales, const void* w, dtype dt, int64_t n,
+                            int64_t k, int group_size = 128, int block_n = 128,
+                            void* stream = nullptr);
 
 }  // namespace inferop

@@ -9,4 +9,5 @@ from ._lib import LIB_PATH, LibraryNotBuilt, lib  # noqa: F401
 from .ops import (  # noqa: F401
     InferopError, Status, dequant_fp8_per_token_group, dequantize, device_count, device_name,
     device_sm_version, dtype, gemm, gemm_config_name, gemm_num_configs, gemm_select, has_cuda,
-    quant_fp8_per_token_group, quantize, w8a8_block_fp8_gemm, w8a8_block_fp8_gemm_config)
+    quant_fp8_per_token_group, quant_fp8_weight_block, quantize, quantize_weight,
+    w8a8_block_fp8_gemm, w8a8_block_fp8_gemm_config)

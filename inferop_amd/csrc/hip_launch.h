@@ -26,6 +26,10 @@ int inferop_hip_quant_fp8_group(void* q, float* scales, const void* x, int32_t d
                                 int64_t cols, int32_t group_size, void* stream);
 int inferop_hip_dequant_fp8_group(void* x, int32_t dt, const uint8_t* q, const float* scales,
                                   int64_t rows, int64_t cols, int32_t group_size, void* stream);
+/* 128 x 128 weight blocks of w [n, k] (k % 128 == 0); w 16-byte, q 8-byte
+ * aligned (hipErrorInvalidValue otherwise). */
+int inferop_hip_weight_block_quant(uint8_t* q, float* scales, const void* w, int32_t dt, int64_t n,
+                                   int64_t k, void* stream);
 
 /* ---- blockwise FP8 GEMM ----
  * cfg: index into the kernel table (inferop_hip_gemm_num_configs());
@@ -40,7 +44,7 @@ typedef struct {
   int32_t bn;     /* block tile along N */
   int32_t bm;     /* block tile along M */
   int32_t waves;  /* waves per workgroup */
-  int32_t kind;   /* 0 = register-staged LDS pipeline, 1 = direct-to-LDS pipeline */
+  int32_t kind;   /* 1 = decode (16-row weight stripes), 2 = LDS-staged output tiles */
   const char* name;
 } inferop_gemm_cfg_info;
 

@@ -193,6 +193,20 @@ int dequant_impl(void* x, int32_t dt, const void* q, const void* scales, int64_t
                                                      group_size, stream));
 }
 
+int weight_quant_impl(void* b_q, void* b_scales, const void* w, int32_t dt, int64_t n, int64_t k,
+                      int32_t group_size, int32_t block_n, void* stream) {
+  if (group_size != 128 || block_n != 128 || n <= 0 || k <= 0 || k % 128 != 0)
+    return INFEROP_ERR_SHAPE;
+  if (!valid_input_dtype(dt)) return INFEROP_ERR_DTYPE;
+  if (reinterpret_cast<uintptr_t>(w) % 16 != 0 || reinterpret_cast<uintptr_t>(b_q) % 8 != 0 ||
+      reinterpret_cast<uintptr_t>(b_scales) % 4 != 0)
+    return INFEROP_ERR_ARGUMENT;
+  if (!current_device()) return INFEROP_ERR_DEVICE;
+  return status_of_hip(inferop_hip_weight_block_quant(static_cast<uint8_t*>(b_q),
+                                                      static_cast<float*>(b_scales), w, dt, n, k,
+                                                      stream));
+}
+
 bool gemm_shape_ok(int64_t m, int64_t n, int64_t k, int32_t group_size, int32_t block_n) {
   // reference w8a8_block_fp8.cu:167-173, including its diagnostic line.
   if (group_size != 128 || block_n != 128 || k % 128 != 0 || m <= 0 || n <= 0) {
@@ -279,6 +293,11 @@ void w8a8_block_fp8_gemm(void* c, const void* a_q, const void* a_scales, const v
                   int32_t(out_dt), stream);
 }
 
+void quant_fp8_weight_block(void* b_q, void* b_scales, const void* w, dtype dt, int64_t n,
+                            int64_t k, int group_size, int block_n, void* stream) {
+  (void)weight_quant_impl(b_q, b_scales, w, int32_t(dt), n, k, group_size, block_n, stream);
+}
+
 }  // namespace inferop
 
 // ---- inferop_c.h ------------------------------------------------------------------
@@ -318,6 +337,12 @@ extern "C" int inferop_w8a8_block_fp8_gemm(void* c, const void* a_q, const void*
                                            int64_t n, int64_t k, int32_t group_size,
                                            int32_t block_n, int32_t out_dt, void* stream) {
   return gemm_impl(c, a_q, a_scales, b_q, b_scales, m, n, k, group_size, block_n, out_dt, stream);
+}
+
+extern "C" int inferop_quant_fp8_weight_block(void* b_q, void* b_scales, const void* w, int32_t dt,
+                                              int64_t n, int64_t k, int32_t group_size,
+                                              int32_t block_n, void* stream) {
+  return weight_quant_impl(b_q, b_scales, w, dt, n, k, group_size, block_n, stream);
 }
 
 extern "C" int inferop_gemm_num_configs(void) { return inferop_hip_gemm_num_configs(); }

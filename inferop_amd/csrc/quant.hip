@@ -296,6 +296,131 @@ hipError_t launch_dequant(void* x, const uint8_t* q, const float* scales, int64_
   return hipGetLastError();
 }
 
+
+// ---- weight block quantizer: one 128 x 128 block of W [N, K] per workgroup ------
+// Semantics (the weight recipe of the reference's GEMM tests,
+// tests/test_gemm.cpp:28-45): per block, absmax over its rows (ignoring NaN),
+// scale = absmax == 0 ? 1 : absmax * fl32(1/448), inv = 1 / scale (IEEE), and
+// q = e4m3_rn_sat(w * inv) -- a product with the reciprocal, not a quotient.
+// Thread t owns 8 consecutive columns (t % 16) of rows t / 16 + 16 i.  Blocks
+// whose absmax is Inf/NaN or below 2^-80 take the slow path (software encoder,
+// x86-64 NaN results, as in the per-token quantizer); elsewhere |w * inv| <=
+// 448 and products are never subnormal, so the hardware multiply and encode
+// are exact.
+
+// Reference-exact code of w * inv for any w and inv.
+__device__ __forceinline__ uint32_t slow_code_mul(float w, float inv) {
+  if (w != w) return ((f2u(w) >> 24) & 0x80u) | 0x7Fu;
+  const float p = w * inv;
+  if (p != p) return 0xFFu;
+  return sw_e4m3(p);
+}
+
+__device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* red) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o));
+  __syncthreads();  // red[] may still be read by an earlier reduction
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return max(max(red[0], red[1]), max(red[2], red[3]));
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void weight_block_quant_kernel(uint8_t* __restrict__ q,
+                                                                 float* __restrict__ scales,
+                                                                 const void* __restrict__ w,
+                                                                 int64_t n, int64_t k) {
+  __shared__ uint32_t red[4];
+  constexpr int kRows = 8;  // rows per thread
+  const int t = threadIdx.x;
+  const int c = t & 15;
+  const int64_t kg = k >> 7;
+  const int64_t g = blockIdx.x, nb = blockIdx.y;
+  const int64_t col = g * 128 + c * 8;
+  float v[kRows][8];
+  uint32_t key = 0;
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) {
+    const int64_t row = nb * 128 + (t >> 4) + 16 * i;
+    if (row < n) {
+      const int64_t e = row * k + col;
+      if constexpr (DT == kFp32) {
+        const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(w) + e);
+        const u32x4 a = p[0], b = p[1];
+        const uint32_t ws[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[i][j] = u2f(ws[j]);
+      } else {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(w) + e);
+        const uint32_t ws[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if constexpr (DT == kBf16) {
+            v[i][2 * j] = u2f(ws[j] << 16);
+            v[i][2 * j + 1] = u2f(ws[j] & 0xFFFF0000u);
+          } else {
+            v[i][2 * j] = (float)__builtin_bit_cast(_Float16, (uint16_t)ws[j]);
+            v[i][2 * j + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(ws[j] >> 16));
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[i][j] = 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) key = max(key, f2u(v[i][j]) & 0x7FFFFFFFu);
+  }
+  key = block_max_u32(key, red);
+  const bool slow = key >= 0x7F800000u || (key != 0 && key < kFastMinAbsmaxBits);
+  float s;
+  if (!slow) {
+    s = (key == 0) ? 1.0f : u2f(key) * kInv448;
+    const float inv = 1.0f / s;
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) {
+      const int64_t row = nb * 128 + (t >> 4) + 16 * i;
+      if (row < n) {
+        const uint32_t lo = cvt_pk4_e4m3(v[i][0] * inv, v[i][1] * inv, v[i][2] * inv, v[i][3] * inv);
+        const uint32_t hi = cvt_pk4_e4m3(v[i][4] * inv, v[i][5] * inv, v[i][6] * inv, v[i][7] * inv);
+        *reinterpret_cast<u32x2*>(q + row * k + col) = u32x2{lo, hi};
+      }
+    }
+  } else {
+    uint32_t k2 = 0;
+#pragma unroll
+    for (int i = 0; i < kRows; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) k2 = max(k2, mag_nonan(v[i][j]));
+    k2 = block_max_u32(k2, red);
+    s = (k2 == 0) ? 1.0f : u2f(k2) * kInv448;
+    const float inv = 1.0f / s;
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) {
+      const int64_t row = nb * 128 + (t >> 4) + 16 * i;
+      if (row < n) {
+        uint32_t cd[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) cd[j] = slow_code_mul(v[i][j], inv);
+        *reinterpret_cast<u32x2*>(q + row * k + col) =
+            u32x2{cd[0] | (cd[1] << 8) | (cd[2] << 16) | (cd[3] << 24),
+                  cd[4] | (cd[5] << 8) | (cd[6] << 16) | (cd[7] << 24)};
+      }
+    }
+  }
+  if (t == 0) scales[nb * kg + g] = s;
+}
+
+template <int DT>
+hipError_t launch_weight_quant(uint8_t* q, float* scales, const void* w, int64_t n, int64_t k,
+                               hipStream_t st) {
+  const int64_t kg = k / 128, nb = (n + 127) / 128;
+  if (kg > 0x7FFFFFFF || nb > 65535) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL((weight_block_quant_kernel<DT>), dim3((unsigned)kg, (unsigned)nb), dim3(256), 0,
+                     st, q, scales, w, n, k);
+  return hipGetLastError();
+}
+
 }  // namespace
 }  // namespace inferop_hip
 
@@ -321,6 +446,20 @@ extern "C" int inferop_hip_dequant_fp8_group(void* x, int32_t dt, const uint8_t*
     case kFp32: return launch_dequant<kFp32>(x, q, scales, rows, cols, group_size, st);
     case kFp16: return launch_dequant<kFp16>(x, q, scales, rows, cols, group_size, st);
     case kBf16: return launch_dequant<kBf16>(x, q, scales, rows, cols, group_size, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+extern "C" int inferop_hip_weight_block_quant(uint8_t* q, float* scales, const void* w, int32_t dt,
+                                              int64_t n, int64_t k, void* stream) {
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // the kernel loads 16 bytes and stores 8 bytes per row segment
+  if ((uintptr_t)w % 16 != 0 || (uintptr_t)q % 8 != 0 || (uintptr_t)scales % 4 != 0)
+    return hipErrorInvalidValue;
+  switch (dt) {
+    case kFp32: return launch_weight_quant<kFp32>(q, scales, w, n, k, st);
+    case kFp16: return launch_weight_quant<kFp16>(q, scales, w, n, k, st);
+    case kBf16: return launch_weight_quant<kBf16>(q, scales, w, n, k, st);
     default: return hipErrorInvalidValue;
   }
 }

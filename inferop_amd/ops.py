@@ -104,6 +104,14 @@ def w8a8_block_fp8_gemm(c, a_q, a_scales, b_q, b_scales, m: int, n: int, k: int,
         block_n, int(out_dt), _stream(stream))
 
 
+# ---- extension: weight block quantizer (the reference's test recipe,
+# tests/test_gemm.cpp:28-45; no counterpart in its ops.h) ---------------------------
+def quant_fp8_weight_block(b_q, b_scales, w, dt, n: int, k: int, group_size: int = 128,
+                           block_n: int = 128, stream=None) -> int:
+    return lib().inferop_quant_fp8_weight_block(
+        _ptr(b_q), _ptr(b_scales), _ptr(w), int(dt), n, k, group_size, block_n, _stream(stream))
+
+
 # ---- tuning entry points (no reference counterpart) ------------------------------
 def gemm_num_configs() -> int:
     return lib().inferop_gemm_num_configs()
@@ -150,6 +158,20 @@ def quantize(x, group_size: int = 128, stream=None):
                                    stream)
     if st != Status.OK:
         raise InferopError(st, "quant_fp8_per_token_group")
+    return q, s
+
+
+def quantize_weight(w, stream=None):
+    """w: [n, k] fp32/fp16/bf16 device tensor -> (b_q uint8 [n, k], b_scales fp32
+    [ceil(n/128), k/128]), the weight format the GEMM consumes."""
+    import torch
+    n, k = w.shape
+    w = w.contiguous()
+    q = torch.empty((n, k), dtype=torch.uint8, device=w.device)
+    s = torch.empty(((n + 127) // 128, k // 128), dtype=torch.float32, device=w.device)
+    st = quant_fp8_weight_block(q, s, w, _torch_dtype_code(w.dtype), n, k, 128, 128, stream)
+    if st != Status.OK:
+        raise InferopError(st, "quant_fp8_weight_block")
     return q, s
 
 

@@ -119,6 +119,13 @@ def test_quant_guards_without_touching_memory():
     d = inferop_amd.dequant_fp8_per_token_group
     assert d(0, inferop_amd.dtype.fp32, 0, 0, 4, 130, 128) == S.ERR_SHAPE
     assert d(0, inferop_amd.dtype.fp8_e4m3, 0, 0, 4, 128, 128) == S.ERR_DTYPE
+    w = inferop_amd.quant_fp8_weight_block
+    assert w(0, 0, 0, inferop_amd.dtype.fp32, 128, 100) == S.ERR_SHAPE
+    assert w(0, 0, 0, inferop_amd.dtype.fp32, 0, 128) == S.ERR_SHAPE
+    assert w(0, 0, 0, inferop_amd.dtype.fp32, 128, 128, group_size=64) == S.ERR_SHAPE
+    assert w(0, 0, 0, inferop_amd.dtype.fp32, 128, 128, block_n=256) == S.ERR_SHAPE
+    assert w(0, 0, 0, inferop_amd.dtype.fp8_e4m3, 128, 128) == S.ERR_DTYPE
+    assert w(16, 0, 8, inferop_amd.dtype.bf16, 128, 128) == S.ERR_ARGUMENT
 
 
 def test_gemm_guards_print_reference_diagnostic(capfd):

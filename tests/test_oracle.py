@@ -237,3 +237,54 @@ def test_weight_block_quant_properties():
             assert qb[i] & 0x7F == 0x7E
             deq = oracle.e4m3_decode_table()[qb] * bs[nb, g]
             assert (np.abs(deq - blk) <= np.maximum(np.abs(blk) / 16, bs[nb, g] * 1.5e-3) + 1e-30).all()
+
+
+def _find_mul_div_splits(count: int, seed: int = 7):
+    """(absmax, x) pairs where e4m3(fl(x * fl(1/s))) != e4m3(fl(x / s)) for the
+    block scale s = fl(absmax * fl(1/448)): values sitting at an E4M3 rounding
+    midpoint, where the reciprocal product and the quotient round apart."""
+    g = np.random.default_rng(seed)
+    L = oracle.lib()
+    mids = [1.0625, 1.1875, 1.3125, 1.4375, 2.125, 2.375, 3.25, 5.5, 9.0, 13.0, 0.53125]
+    out = []
+    inv448 = np.float32(1) / np.float32(448)
+    while len(out) < count:
+        amax = np.float32(g.uniform(0.01, 10.0))
+        s = np.float32(amax * inv448)
+        inv = np.float32(np.float32(1) / s)
+        for t in mids:
+            for d in (-1, 0, 1):
+                x = np.nextafter(np.float32(t * s), np.float32(np.inf if d > 0 else -np.inf)) \
+                    if d else np.float32(t * s)
+                if abs(x) > amax:
+                    continue
+                cm = L.orc_grid_encode(float(np.float32(x * inv)))
+                cd = L.orc_grid_encode(float(np.float32(x / s)))
+                if cm != cd:
+                    out.append((amax, np.float32(x)))
+    return out[:count]
+
+
+def test_weight_block_quant_multiplies_by_reciprocal():
+    # tests/test_gemm.cpp:38-42: w * (1 / scale), not w / scale.  Every block
+    # holds its absmax plus values for which the two round to different E4M3
+    # codes; the expected bytes come from numpy float32 products and the
+    # independent grid encoder.
+    pairs = _find_mul_div_splits(24)
+    L = oracle.lib()
+    w = np.zeros((128, 128 * len(pairs)), np.float32)
+    for b, (amax, x) in enumerate(pairs):
+        w[0, b * 128] = amax
+        w[1:, b * 128 + 1] = x
+        w[5, b * 128 + 7] = -x
+    bq, bs = oracle.weight_block_quant(w)
+    inv448 = np.float32(1) / np.float32(448)
+    differ = 0
+    for b, (amax, x) in enumerate(pairs):
+        s = np.float32(amax * inv448)
+        assert bs[0, b] == s
+        inv = np.float32(np.float32(1) / s)
+        for v, (r, c) in ((x, (1, b * 128 + 1)), (-x, (5, b * 128 + 7)), (amax, (0, b * 128))):
+            assert bq[r, c] == L.orc_grid_encode(float(np.float32(v * inv))), (amax, v)
+            differ += bq[r, c] != L.orc_grid_encode(float(np.float32(v / s)))
+    assert differ >= len(pairs)
