@@ -69,6 +69,18 @@ int inferop_w8a8_block_fp8_gemm(void* c, const void* a_q, const void* a_scales, 
 int inferop_quant_fp8_weight_block(void* b_q, void* b_scales, const void* w, int32_t dt, int64_t n,
                                    int64_t k, int32_t group_size, int32_t block_n, void* stream);
 
+/* --- extension: producers fused with the per-token-group quantizer (no
+ * counterparts in the reference ops.h; see inferop::silu_and_mul_quant_fp8 and
+ * inferop::fused_add_rmsnorm_quant_fp8 in ops.h).  group_size != 128,
+ * tokens/rows <= 0, d/cols <= 0 or not a multiple of 128 return
+ * INFEROP_ERR_SHAPE; dt outside {fp32, fp16, bf16} INFEROP_ERR_DTYPE; a dt
+ * tensor not 16-byte aligned or q not 8-byte aligned INFEROP_ERR_ARGUMENT. */
+int inferop_silu_and_mul_quant_fp8(void* q, void* scales, const void* gate_up, int32_t dt,
+                                   int64_t tokens, int64_t d, int32_t group_size, void* stream);
+int inferop_fused_add_rmsnorm_quant_fp8(void* residual, void* q, void* scales, const void* x,
+                                        const void* weight, int32_t dt, int64_t rows, int64_t cols,
+                                        float eps, int32_t group_size, void* stream);
+
 /* --- tuning and testing (no counterpart in the reference) ---
  * The GEMM with an explicit kernel configuration and split-K factor instead
  * of the automatic gfx950 choice.  config in [0, inferop_gemm_num_configs()). */

@@ -4,8 +4,9 @@
 // function below has the reference's exact C++ signature and default arguments, so the
 // Itanium-mangled symbols exported by libinferop.so are the ones a program
 // built against the reference links to.  Only the FP8 path is provided
-// (quantizer, dequantizer, blockwise GEMM) plus device introspection, and one
-// extension the reference keeps in its tests: the weight block quantizer.
+// (quantizer, dequantizer, blockwise GEMM) plus device introspection, and
+// three extensions: the weight block quantizer the reference keeps in its
+// tests, and the two producers of the quantizer's input fused with it.
 //
 // All tensors are caller-owned device pointers.  `stream` is an opaque
 // hipStream_t; nullptr is the null stream.  Calls are asynchronous on that
@@ -73,5 +74,26 @@ void w8a8_block_fp8_gemm(void* c, const void* a_q, const void* a_scales, const v
 void quant_fp8_weight_block(void* b_q, void* b_scales, const void* w, dtype dt, int64_t n,
                             int64_t k, int group_size = 128, int block_n = 128,
                             void* stream = nullptr);
+
+// --- extension: producers fused with the per-token-group quantizer -----------
+// No counterparts in the reference ops.h, which runs these as separate calls:
+// silu_and_mul (ops.h:51-55) or fused_add_rmsnorm (ops.h:33-37) writing dt,
+// then quant_fp8_per_token_group on that output.  The fused calls produce the
+// same q / scales as that sequence would from the dt values it stores, without
+// the dt tensor in HBM.  group_size must be 128 and d / cols multiples of 128;
+// dt tensors 16-byte aligned, q 8-byte aligned; other calls are no-ops.
+//
+//   gate_up: [tokens, 2d] dt -> q [tokens, d] E4M3, scales [tokens, d/128]
+//   out = silu(gate_up[:, :d]) * gate_up[:, d:]   (reference.cpp:55-64)
+void silu_and_mul_quant_fp8(void* q, void* scales, const void* gate_up, dtype dt, int64_t tokens,
+                            int64_t d, int group_size = 128, void* stream = nullptr);
+
+//   residual [rows, cols] dt, updated in place: residual += x
+//   q [rows, cols] E4M3, scales [rows, cols/128] of rmsnorm(residual) * weight
+//   (reference.cpp:23-35; eps as in the reference's default)
+void fused_add_rmsnorm_quant_fp8(void* residual, void* q, void* scales, const void* x,
+                                 const void* weight, dtype dt, int64_t rows, int64_t cols,
+                                 float eps = 1e-6f, int group_size = 128,
+                                 void* stream = nullptr);
 
 }  // namespace inferop

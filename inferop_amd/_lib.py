@@ -32,6 +32,9 @@ C_API = [
      [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _i32, _vp]),
     ("inferop_quant_fp8_weight_block", ctypes.c_int,
      [_vp, _vp, _vp, _i32, _i64, _i64, _i32, _i32, _vp]),
+    ("inferop_silu_and_mul_quant_fp8", ctypes.c_int, [_vp, _vp, _vp, _i32, _i64, _i64, _i32, _vp]),
+    ("inferop_fused_add_rmsnorm_quant_fp8", ctypes.c_int,
+     [_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, ctypes.c_float, _i32, _vp]),
     ("inferop_gemm_num_configs", ctypes.c_int, []),
     ("inferop_gemm_config_name", ctypes.c_char_p, [ctypes.c_int]),
     ("inferop_w8a8_block_fp8_gemm_config", ctypes.c_int,

@@ -31,6 +31,14 @@ int inferop_hip_dequant_fp8_group(void* x, int32_t dt, const uint8_t* q, const f
 int inferop_hip_weight_block_quant(uint8_t* q, float* scales, const void* w, int32_t dt, int64_t n,
                                    int64_t k, void* stream);
 
+/* ---- fused producers + quantizer (d, cols multiples of 128; dt inputs
+ * 16-byte aligned, q 8-byte aligned) ---- */
+int inferop_hip_silu_mul_quant(uint8_t* q, float* scales, const void* gate_up, int32_t dt,
+                               int64_t tokens, int64_t d, void* stream);
+int inferop_hip_add_rmsnorm_quant(void* residual, uint8_t* q, float* scales, const void* x,
+                                  const void* weight, int32_t dt, int64_t rows, int64_t cols,
+                                  float eps, void* stream);
+
 /* ---- blockwise FP8 GEMM ----
  * cfg: index into the kernel table (inferop_hip_gemm_num_configs());
  * split_k: number of K partitions (1 = none); partitions > 1 reduce through

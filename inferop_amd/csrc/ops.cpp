@@ -207,6 +207,33 @@ int weight_quant_impl(void* b_q, void* b_scales, const void* w, int32_t dt, int6
                                                       stream));
 }
 
+bool aligned(const void* p, uintptr_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; }
+
+int silu_quant_impl(void* q, void* scales, const void* gate_up, int32_t dt, int64_t tokens,
+                    int64_t d, int32_t group_size, void* stream) {
+  if (group_size != 128 || tokens <= 0 || d <= 0 || d % 128 != 0) return INFEROP_ERR_SHAPE;
+  if (!valid_input_dtype(dt)) return INFEROP_ERR_DTYPE;
+  if (!aligned(gate_up, 16) || !aligned(q, 8) || !aligned(scales, 4)) return INFEROP_ERR_ARGUMENT;
+  if (!current_device()) return INFEROP_ERR_DEVICE;
+  return status_of_hip(inferop_hip_silu_mul_quant(static_cast<uint8_t*>(q),
+                                                  static_cast<float*>(scales), gate_up, dt, tokens,
+                                                  d, stream));
+}
+
+int rmsnorm_quant_impl(void* residual, void* q, void* scales, const void* x, const void* weight,
+                       int32_t dt, int64_t rows, int64_t cols, float eps, int32_t group_size,
+                       void* stream) {
+  if (group_size != 128 || rows <= 0 || cols <= 0 || cols % 128 != 0) return INFEROP_ERR_SHAPE;
+  if (!valid_input_dtype(dt)) return INFEROP_ERR_DTYPE;
+  if (!aligned(residual, 16) || !aligned(x, 16) || !aligned(weight, 16) || !aligned(q, 8) ||
+      !aligned(scales, 4))
+    return INFEROP_ERR_ARGUMENT;
+  if (!current_device()) return INFEROP_ERR_DEVICE;
+  return status_of_hip(inferop_hip_add_rmsnorm_quant(residual, static_cast<uint8_t*>(q),
+                                                     static_cast<float*>(scales), x, weight, dt,
+                                                     rows, cols, eps, stream));
+}
+
 bool gemm_shape_ok(int64_t m, int64_t n, int64_t k, int32_t group_size, int32_t block_n) {
   // reference w8a8_block_fp8.cu:167-173, including its diagnostic line.
   if (group_size != 128 || block_n != 128 || k % 128 != 0 || m <= 0 || n <= 0) {
@@ -298,6 +325,18 @@ void quant_fp8_weight_block(void* b_q, void* b_scales, const void* w, dtype dt, 
   (void)weight_quant_impl(b_q, b_scales, w, int32_t(dt), n, k, group_size, block_n, stream);
 }
 
+void silu_and_mul_quant_fp8(void* q, void* scales, const void* gate_up, dtype dt, int64_t tokens,
+                            int64_t d, int group_size, void* stream) {
+  (void)silu_quant_impl(q, scales, gate_up, int32_t(dt), tokens, d, group_size, stream);
+}
+
+void fused_add_rmsnorm_quant_fp8(void* residual, void* q, void* scales, const void* x,
+                                 const void* weight, dtype dt, int64_t rows, int64_t cols,
+                                 float eps, int group_size, void* stream) {
+  (void)rmsnorm_quant_impl(residual, q, scales, x, weight, int32_t(dt), rows, cols, eps,
+                           group_size, stream);
+}
+
 }  // namespace inferop
 
 // ---- inferop_c.h ------------------------------------------------------------------
@@ -343,6 +382,20 @@ extern "C" int inferop_quant_fp8_weight_block(void* b_q, void* b_scales, const v
                                               int64_t n, int64_t k, int32_t group_size,
                                               int32_t block_n, void* stream) {
   return weight_quant_impl(b_q, b_scales, w, dt, n, k, group_size, block_n, stream);
+}
+
+extern "C" int inferop_silu_and_mul_quant_fp8(void* q, void* scales, const void* gate_up,
+                                              int32_t dt, int64_t tokens, int64_t d,
+                                              int32_t group_size, void* stream) {
+  return silu_quant_impl(q, scales, gate_up, dt, tokens, d, group_size, stream);
+}
+
+extern "C" int inferop_fused_add_rmsnorm_quant_fp8(void* residual, void* q, void* scales,
+                                                   const void* x, const void* weight, int32_t dt,
+                                                   int64_t rows, int64_t cols, float eps,
+                                                   int32_t group_size, void* stream) {
+  return rmsnorm_quant_impl(residual, q, scales, x, weight, dt, rows, cols, eps, group_size,
+                            stream);
 }
 
 extern "C" int inferop_gemm_num_configs(void) { return inferop_hip_gemm_num_configs(); }

@@ -108,6 +108,44 @@ __device__ __forceinline__ uint32_t slow_code(float x, float s) {
   return sw_e4m3(qv);
 }
 
+// Quantize the 128-element group held by the 16 lanes of one DPP row, each
+// lane owning 8 consecutive elements as raw dt words w[]: returns this lane's
+// 8 codes (lo = elements 0-3, hi = 4-7) and the group scale.  Every lane of
+// the wave must call it (the absmax reduction is a row-wide DPP exchange).
+template <int DT>
+__device__ __forceinline__ void quant_group_lane(const uint32_t* w, uint32_t& lo, uint32_t& hi,
+                                                 float& s) {
+  using I = In<DT>;
+  uint32_t key = row16_max_u32(I::key(w));
+  float amax = I::key_to_float(key);
+  s = (key == 0) ? 1.0f : amax * kInv448;
+  const bool slow = key >= I::kInfKey || (key != 0 && f2u(amax) < kFastMinAbsmaxBits);
+  if (!slow) {
+    float v[8];
+    if constexpr (DT == kFp32) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = I::elem(w, i) / s;
+    } else {
+      const float r = 1.0f / s;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = inferop_qmath::div_by_recip(I::elem(w, i), s, r);
+    }
+    lo = cvt_pk4_e4m3(v[0], v[1], v[2], v[3]);
+    hi = cvt_pk4_e4m3(v[4], v[5], v[6], v[7]);
+  } else {
+    uint32_t k2 = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) k2 = max(k2, mag_nonan(I::elem(w, i)));
+    k2 = row16_max_u32(k2);
+    s = (k2 == 0) ? 1.0f : u2f(k2) * kInv448;
+    uint32_t c[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) c[i] = slow_code(I::elem(w, i), s);
+    lo = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+    hi = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
+  }
+}
+
 template <int DT, int U>
 __global__ __launch_bounds__(256) void quant_g128_kernel(uint8_t* __restrict__ q,
                                                          float* __restrict__ scales,
@@ -144,35 +182,9 @@ __global__ __launch_bounds__(256) void quant_g128_kernel(uint8_t* __restrict__ q
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int64_t g = g0 + 4 * u;
-    uint32_t key = row16_max_u32(I::key(w[u]));
-    float amax = I::key_to_float(key);
-    float s = (key == 0) ? 1.0f : amax * kInv448;
     uint32_t lo, hi;
-    const bool slow = key >= I::kInfKey || (key != 0 && f2u(amax) < kFastMinAbsmaxBits);
-    if (!slow) {
-      float v[8];
-      if constexpr (DT == kFp32) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = I::elem(w[u], i) / s;
-      } else {
-        const float r = 1.0f / s;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = inferop_qmath::div_by_recip(I::elem(w[u], i), s, r);
-      }
-      lo = cvt_pk4_e4m3(v[0], v[1], v[2], v[3]);
-      hi = cvt_pk4_e4m3(v[4], v[5], v[6], v[7]);
-    } else {
-      uint32_t k2 = 0;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) k2 = max(k2, mag_nonan(I::elem(w[u], i)));
-      k2 = row16_max_u32(k2);
-      s = (k2 == 0) ? 1.0f : u2f(k2) * kInv448;
-      uint32_t c[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) c[i] = slow_code(I::elem(w[u], i), s);
-      lo = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
-      hi = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
-    }
+    float s;
+    quant_group_lane<DT>(w[u], lo, hi, s);
     if (g < ngroups) {
       u32x2* dst = reinterpret_cast<u32x2*>(q + g * 128 + sub * 8);
       __builtin_nontemporal_store(u32x2{lo, hi}, dst);
@@ -421,6 +433,193 @@ hipError_t launch_weight_quant(uint8_t* q, float* scales, const void* w, int64_t
   return hipGetLastError();
 }
 
+
+// ---- fused producers: the layer output is quantized without a dt round trip ----
+// Each computes the producer in fp32, rounds the value to the storage type dt
+// exactly where the unfused path stores it (round to nearest even: the
+// hardware conversions (__bf16) / (_Float16), i.e. __float2bfloat16 /
+// __float2half of the reference kernels), and quantizes that value with the
+// per-token-group quantizer above -- bytes and scales are those of
+// quant_fp8_per_token_group applied to the stored producer output.
+
+// 8 fp32 values rounded to dt, packed as the raw words quant_group_lane reads.
+template <int DT>
+__device__ __forceinline__ void pack_dt8(const float* v, uint32_t* w) {
+  if constexpr (DT == kFp32) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = f2u(v[i]);
+  } else if constexpr (DT == kBf16) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = uint32_t(__builtin_bit_cast(uint16_t, (__bf16)v[2 * i])) |
+             (uint32_t(__builtin_bit_cast(uint16_t, (__bf16)v[2 * i + 1])) << 16);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = uint32_t(__builtin_bit_cast(uint16_t, (_Float16)v[2 * i])) |
+             (uint32_t(__builtin_bit_cast(uint16_t, (_Float16)v[2 * i + 1])) << 16);
+  }
+}
+
+// 8 consecutive dt elements at p (16-byte aligned for 16-bit types, 32 for fp32).
+template <int DT>
+__device__ __forceinline__ void load_dt8(const void* p, float* v) {
+  if constexpr (DT == kFp32) {
+    const u32x4* q = reinterpret_cast<const u32x4*>(p);
+    const u32x4 a = q[0], b = q[1];
+    v[0] = u2f(a.x), v[1] = u2f(a.y), v[2] = u2f(a.z), v[3] = u2f(a.w);
+    v[4] = u2f(b.x), v[5] = u2f(b.y), v[6] = u2f(b.z), v[7] = u2f(b.w);
+  } else {
+    const u32x4 a = *reinterpret_cast<const u32x4*>(p);
+    const uint32_t ws[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (DT == kBf16) {
+        v[2 * i] = u2f(ws[i] << 16);
+        v[2 * i + 1] = u2f(ws[i] & 0xFFFF0000u);
+      } else {
+        v[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)ws[i]);
+        v[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(ws[i] >> 16));
+      }
+    }
+  }
+}
+
+// SiLU(g) * u with the reference's fp32 operation order
+// (reference/reference.cpp:60-61: (g / (1 + exp(-g))) * u).  exp(-g) is
+// evaluated in double precision and rounded once to fp32, which gives the
+// correctly rounded fp32 exponential except where the double result lies
+// within 2^-29 relative of an fp32 rounding midpoint.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  const float e = (float)::exp(-(double)g);
+  return (g / (1.0f + e)) * u;
+}
+
+// gate_up: [tokens, 2d] dt -> q [tokens, d] E4M3, scales [tokens, d/128].
+// Lane layout as quant_g128_kernel: 16 lanes per 128-output group.
+template <int DT>
+__global__ __launch_bounds__(256) void silu_mul_quant_kernel(uint8_t* __restrict__ q,
+                                                             float* __restrict__ scales,
+                                                             const void* __restrict__ gate_up,
+                                                             int64_t d, int64_t ngroups) {
+  constexpr int EB = DT == kFp32 ? 4 : 2;
+  const int lane = threadIdx.x & 63;
+  const int sub = lane & 15;
+  const int64_t g = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 4 + (lane >> 4);
+  const int64_t gpr = d >> 7;
+  const bool live = g < ngroups;
+  const int64_t t = live ? g / gpr : 0, gc = live ? g - t * gpr : 0;
+  float gv[8], uv[8], y[8];
+  if (live) {
+    const uint8_t* row = reinterpret_cast<const uint8_t*>(gate_up) + t * 2 * d * EB;
+    load_dt8<DT>(row + (gc * 128 + sub * 8) * EB, gv);
+    load_dt8<DT>(row + (d + gc * 128 + sub * 8) * EB, uv);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = silu_mul(gv[i], uv[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = 0.0f;
+  }
+  uint32_t w[In<DT>::kWords];
+  pack_dt8<DT>(y, w);
+  uint32_t lo, hi;
+  float s;
+  quant_group_lane<DT>(w, lo, hi, s);
+  if (live) {
+    *reinterpret_cast<u32x2*>(q + t * d + gc * 128 + sub * 8) = u32x2{lo, hi};
+    if (sub == 0) scales[g] = s;
+  }
+}
+
+// One workgroup per row: residual = dt(residual + x) in place, then
+// out = dt((residual * inv_rms) * weight) quantized per 128-column group
+// (reference/reference.cpp:23-35 for the arithmetic; the sum of squares is a
+// tree over the stored residual values, the reference's is left to right).
+template <int DT>
+__global__ __launch_bounds__(256) void add_rmsnorm_quant_kernel(
+    void* __restrict__ residual, uint8_t* __restrict__ q, float* __restrict__ scales,
+    const void* __restrict__ x, const void* __restrict__ weight, int64_t cols, float eps) {
+  constexpr int EB = DT == kFp32 ? 4 : 2;
+  __shared__ float red[4];
+  const int t = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  uint8_t* res = reinterpret_cast<uint8_t*>(residual) + row * cols * EB;
+  const uint8_t* xr = reinterpret_cast<const uint8_t*>(x) + row * cols * EB;
+  float ss = 0.0f;
+  for (int64_t c = (int64_t)t * 8; c < cols; c += 2048) {
+    float rv[8], xv[8];
+    load_dt8<DT>(res + c * EB, rv);
+    load_dt8<DT>(xr + c * EB, xv);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) rv[i] = rv[i] + xv[i];
+    uint32_t w[In<DT>::kWords];
+    pack_dt8<DT>(rv, w);
+    if constexpr (DT == kFp32) {
+      *reinterpret_cast<u32x4*>(res + c * EB) = u32x4{w[0], w[1], w[2], w[3]};
+      *reinterpret_cast<u32x4*>(res + c * EB + 16) = u32x4{w[4], w[5], w[6], w[7]};
+    } else {
+      *reinterpret_cast<u32x4*>(res + c * EB) = u32x4{w[0], w[1], w[2], w[3]};
+    }
+    float stored[8];
+    load_dt8<DT>(w, stored);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += stored[i] * stored[i];
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+  if ((t & 63) == 0) red[t >> 6] = ss;
+  __syncthreads();
+  ss = (red[0] + red[1]) + (red[2] + red[3]);
+  const float inv = 1.0f / __builtin_sqrtf(ss / (float)cols + eps);
+  const int64_t gpr = cols >> 7;
+  const uint8_t* wt = reinterpret_cast<const uint8_t*>(weight);
+  for (int64_t c0 = 0; c0 < cols; c0 += 2048) {
+    const int64_t c = c0 + (int64_t)t * 8;
+    const bool live = c < cols;  // whole 16-lane groups, since cols % 128 == 0
+    float y[8];
+    if (live) {
+      float rv[8], wv[8];
+      load_dt8<DT>(res + c * EB, rv);  // this thread's own stores above
+      load_dt8<DT>(wt + c * EB, wv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) y[i] = rv[i] * inv * wv[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) y[i] = 0.0f;
+    }
+    uint32_t w[In<DT>::kWords];
+    pack_dt8<DT>(y, w);
+    uint32_t lo, hi;
+    float s;
+    quant_group_lane<DT>(w, lo, hi, s);
+    if (live) {
+      *reinterpret_cast<u32x2*>(q + row * cols + c) = u32x2{lo, hi};
+      if ((t & 15) == 0) scales[row * gpr + (c >> 7)] = s;
+    }
+  }
+}
+
+template <int DT>
+hipError_t launch_silu_mul_quant(uint8_t* q, float* scales, const void* gate_up, int64_t tokens,
+                                 int64_t d, hipStream_t st) {
+  const int64_t ngroups = tokens * (d / 128);
+  const int64_t blocks = (ngroups + 15) / 16;
+  if (blocks > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL((silu_mul_quant_kernel<DT>), dim3((unsigned)blocks), dim3(256), 0, st, q,
+                     scales, gate_up, d, ngroups);
+  return hipGetLastError();
+}
+
+template <int DT>
+hipError_t launch_add_rmsnorm_quant(void* residual, uint8_t* q, float* scales, const void* x,
+                                    const void* weight, int64_t rows, int64_t cols, float eps,
+                                    hipStream_t st) {
+  if (rows > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL((add_rmsnorm_quant_kernel<DT>), dim3((unsigned)rows), dim3(256), 0, st,
+                     residual, q, scales, x, weight, cols, eps);
+  return hipGetLastError();
+}
+
 }  // namespace
 }  // namespace inferop_hip
 
@@ -460,6 +659,32 @@ extern "C" int inferop_hip_weight_block_quant(uint8_t* q, float* scales, const v
     case kFp32: return launch_weight_quant<kFp32>(q, scales, w, n, k, st);
     case kFp16: return launch_weight_quant<kFp16>(q, scales, w, n, k, st);
     case kBf16: return launch_weight_quant<kBf16>(q, scales, w, n, k, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+extern "C" int inferop_hip_silu_mul_quant(uint8_t* q, float* scales, const void* gate_up,
+                                          int32_t dt, int64_t tokens, int64_t d, void* stream) {
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (dt) {
+    case kFp32: return launch_silu_mul_quant<kFp32>(q, scales, gate_up, tokens, d, st);
+    case kFp16: return launch_silu_mul_quant<kFp16>(q, scales, gate_up, tokens, d, st);
+    case kBf16: return launch_silu_mul_quant<kBf16>(q, scales, gate_up, tokens, d, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+extern "C" int inferop_hip_add_rmsnorm_quant(void* residual, uint8_t* q, float* scales,
+                                             const void* x, const void* weight, int32_t dt,
+                                             int64_t rows, int64_t cols, float eps, void* stream) {
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (dt) {
+    case kFp32:
+      return launch_add_rmsnorm_quant<kFp32>(residual, q, scales, x, weight, rows, cols, eps, st);
+    case kFp16:
+      return launch_add_rmsnorm_quant<kFp16>(residual, q, scales, x, weight, rows, cols, eps, st);
+    case kBf16:
+      return launch_add_rmsnorm_quant<kBf16>(residual, q, scales, x, weight, rows, cols, eps, st);
     default: return hipErrorInvalidValue;
   }
 }

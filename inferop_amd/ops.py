@@ -112,6 +112,21 @@ def quant_fp8_weight_block(b_q, b_scales, w, dt, n: int, k: int, group_size: int
         _ptr(b_q), _ptr(b_scales), _ptr(w), int(dt), n, k, group_size, block_n, _stream(stream))
 
 
+# ---- extension: producers fused with the quantizer (the reference runs
+# silu_and_mul / fused_add_rmsnorm, ops.h:33-55, then quant_fp8_per_token_group) ----
+def silu_and_mul_quant_fp8(q, scales, gate_up, dt, tokens: int, d: int, group_size: int = 128,
+                           stream=None) -> int:
+    return lib().inferop_silu_and_mul_quant_fp8(_ptr(q), _ptr(scales), _ptr(gate_up), int(dt),
+                                                tokens, d, group_size, _stream(stream))
+
+
+def fused_add_rmsnorm_quant_fp8(residual, q, scales, x, weight, dt, rows: int, cols: int,
+                                eps: float = 1e-6, group_size: int = 128, stream=None) -> int:
+    return lib().inferop_fused_add_rmsnorm_quant_fp8(
+        _ptr(residual), _ptr(q), _ptr(scales), _ptr(x), _ptr(weight), int(dt), rows, cols,
+        eps, group_size, _stream(stream))
+
+
 # ---- tuning entry points (no reference counterpart) ------------------------------
 def gemm_num_configs() -> int:
     return lib().inferop_gemm_num_configs()

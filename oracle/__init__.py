@@ -68,6 +68,10 @@ def lib():
         L.orc_w8a8_block_fp8_gemm_rows.argtypes = [_f32p, _u8p, _f32p, _u8p, _f32p, _i64, _i64,
                                                    _i64, _i32, _i32, _i64p, _i64, _i32]
         L.orc_weight_block_quant.argtypes = [_u8p, _f32p, _f32p, _i64, _i64, _i32, _i32]
+        L.orc_rmsnorm.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, ctypes.c_float]
+        L.orc_fused_add_rmsnorm.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64, _i64,
+                                            ctypes.c_float]
+        L.orc_silu_and_mul.argtypes = [_f32p, _f32p, _i64, _i64]
         L.orc_sweep_encode_vs_grid.restype = _u64
         L.orc_sweep_encode_vs_grid.argtypes = [_u64, _u64]
         L.orc_encode_checksum.restype = _u64
@@ -101,6 +105,10 @@ def ref():
         R.ref_dequant.argtypes = [_f32p, _u8p, _f32p, _i64, _i64, ctypes.c_int]
         R.ref_gemm.argtypes = [_f32p, _u8p, _f32p, _u8p, _f32p, _i64, _i64, _i64, ctypes.c_int,
                                ctypes.c_int]
+        R.ref_rmsnorm.argtypes = [_f32p, _f32p, _f32p, _i64, _i64, ctypes.c_float]
+        R.ref_fused_add_rmsnorm.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64, _i64,
+                                            ctypes.c_float]
+        R.ref_silu_and_mul.argtypes = [_f32p, _f32p, _i64, _i64]
         _ref = R
     return _ref
 
@@ -193,3 +201,35 @@ def ref_gemm(a_q, a_s, b_q, b_s) -> np.ndarray:
     ref().ref_gemm(_ptr(c, _f32p), _ptr(a_q, _u8p), _ptr(a_s, _f32p), _ptr(b_q, _u8p),
                    _ptr(b_s, _f32p), m, n, k, 128, 128)
     return c
+
+
+def silu_and_mul(gate_up: np.ndarray) -> np.ndarray:
+    """reference.cpp:55-64 on fp32 [tokens, 2d] -> [tokens, d]."""
+    gu = np.ascontiguousarray(gate_up, dtype=np.float32)
+    t, d2 = gu.shape
+    out = np.empty((t, d2 // 2), np.float32)
+    lib().orc_silu_and_mul(_ptr(out, _f32p), _ptr(gu, _f32p), t, d2 // 2)
+    return out
+
+
+def fused_add_rmsnorm(residual: np.ndarray, x: np.ndarray, weight: np.ndarray,
+                      eps: float = 1e-6):
+    """reference.cpp:23-35 -> (new residual, out), inputs untouched."""
+    res = np.array(residual, dtype=np.float32, order="C", copy=True)
+    xr = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(weight, dtype=np.float32)
+    rows, cols = res.shape
+    out = np.empty_like(res)
+    lib().orc_fused_add_rmsnorm(_ptr(res, _f32p), _ptr(out, _f32p), _ptr(xr, _f32p),
+                                _ptr(w, _f32p), rows, cols, eps)
+    return res, out
+
+
+def rmsnorm(x: np.ndarray, weight: np.ndarray, eps: float = 1e-6) -> np.ndarray:
+    """reference.cpp:11-21."""
+    xr = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(weight, dtype=np.float32)
+    rows, cols = xr.shape
+    out = np.empty_like(xr)
+    lib().orc_rmsnorm(_ptr(out, _f32p), _ptr(xr, _f32p), _ptr(w, _f32p), rows, cols, eps)
+    return out

@@ -259,6 +259,48 @@ void orc_weight_block_quant(uint8_t* b_q, float* b_scales, const float* w, int64
   }
 }
 
+/* ---- producers of the quantizer's input (the layers before each GEMM) ----
+ * reference/reference.cpp:11-21, 23-35 and 55-64, loop for loop: the
+ * sum of squares runs left to right in fp32, the inverse RMS is
+ * 1 / sqrtf(ss / cols + eps), the scaling is (x * inv) * w, and SiLU is
+ * g / (1 + expf(-g)) with the C library's expf (the function std::exp(float)
+ * calls on this host).  Pinned against the compiled reference bit for bit. */
+void orc_rmsnorm(float* out, const float* in, const float* weight, int64_t rows, int64_t cols,
+                 float eps) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* x = in + r * cols;
+    float* y = out + r * cols;
+    float ss = 0.0f;
+    for (int64_t c = 0; c < cols; ++c) ss += x[c] * x[c];
+    const float inv = 1.0f / sqrtf(ss / (float)cols + eps);
+    for (int64_t c = 0; c < cols; ++c) y[c] = x[c] * inv * weight[c];
+  }
+}
+
+void orc_fused_add_rmsnorm(float* residual, float* out, const float* x, const float* weight,
+                           int64_t rows, int64_t cols, float eps) {
+  for (int64_t r = 0; r < rows; ++r) {
+    float* res = residual + r * cols;
+    float* y = out + r * cols;
+    const float* xr = x + r * cols;
+    for (int64_t c = 0; c < cols; ++c) res[c] += xr[c];
+    float ss = 0.0f;
+    for (int64_t c = 0; c < cols; ++c) ss += res[c] * res[c];
+    const float inv = 1.0f / sqrtf(ss / (float)cols + eps);
+    for (int64_t c = 0; c < cols; ++c) y[c] = res[c] * inv * weight[c];
+  }
+}
+
+void orc_silu_and_mul(float* out, const float* gate_up, int64_t tokens, int64_t d) {
+  for (int64_t t = 0; t < tokens; ++t) {
+    const float* row = gate_up + t * 2 * d;
+    for (int64_t i = 0; i < d; ++i) {
+      const float g = row[i];
+      out[t * d + i] = (g / (1.0f + expf(-g))) * row[d + i];
+    }
+  }
+}
+
 /* ---- independent encoder: nearest OCP grid point ------------------------- */
 
 /* Positive finite E4M3 values, codes 0x00..0x7E, from the OCP definition

@@ -49,6 +49,15 @@ void orc_w8a8_block_fp8_gemm_rows(float* c, const uint8_t* a_q, const float* a_s
 void orc_weight_block_quant(uint8_t* b_q, float* b_scales, const float* w, int64_t n, int64_t k,
                             int32_t group_size, int32_t block_n);
 
+/* reference/reference.cpp:11-21 (rows x cols fp32, eps as given). */
+void orc_rmsnorm(float* out, const float* in, const float* weight, int64_t rows, int64_t cols,
+                 float eps);
+/* reference/reference.cpp:23-35: residual += x in place, out = rmsnorm(residual). */
+void orc_fused_add_rmsnorm(float* residual, float* out, const float* x, const float* weight,
+                           int64_t rows, int64_t cols, float eps);
+/* reference/reference.cpp:55-64: out[t, i] = silu(gate_up[t, i]) * gate_up[t, d + i]. */
+void orc_silu_and_mul(float* out, const float* gate_up, int64_t tokens, int64_t d);
+
 /* Independent E4M3 encoder: nearest point of the 253-value finite grid built
  * from the OCP definition, ties to the even encoding, |f| >= 448 saturates
  * (tests/test_fp8.cpp:8-50 describes the same oracle).  NaN -> sign|0x7F. */

@@ -58,4 +58,16 @@ void ref_gemm(float* c, const uint8_t* a_q, const float* a_scales, const uint8_t
   inferop::ref::w8a8_block_fp8_gemm(c, a_q, a_scales, b_q, b_scales, m, n, k, gs, bn);
 }
 
+void ref_rmsnorm(float* out, const float* in, const float* w, int64_t rows, int64_t cols,
+                 float eps) {
+  inferop::ref::rmsnorm(out, in, w, rows, cols, eps);
+}
+void ref_fused_add_rmsnorm(float* residual, float* out, const float* x, const float* w,
+                           int64_t rows, int64_t cols, float eps) {
+  inferop::ref::fused_add_rmsnorm(residual, out, x, w, rows, cols, eps);
+}
+void ref_silu_and_mul(float* out, const float* gate_up, int64_t tokens, int64_t d) {
+  inferop::ref::silu_and_mul(out, gate_up, tokens, d);
+}
+
 }  // extern "C"

@@ -126,6 +126,16 @@ def test_quant_guards_without_touching_memory():
     assert w(0, 0, 0, inferop_amd.dtype.fp32, 128, 128, block_n=256) == S.ERR_SHAPE
     assert w(0, 0, 0, inferop_amd.dtype.fp8_e4m3, 128, 128) == S.ERR_DTYPE
     assert w(16, 0, 8, inferop_amd.dtype.bf16, 128, 128) == S.ERR_ARGUMENT
+    f = inferop_amd.silu_and_mul_quant_fp8
+    assert f(0, 0, 0, inferop_amd.dtype.bf16, 4, 200) == S.ERR_SHAPE
+    assert f(0, 0, 0, inferop_amd.dtype.bf16, 0, 256) == S.ERR_SHAPE
+    assert f(0, 0, 0, inferop_amd.dtype.bf16, 4, 256, group_size=64) == S.ERR_SHAPE
+    assert f(0, 0, 0, inferop_amd.dtype.fp8_e4m3, 4, 256) == S.ERR_DTYPE
+    assert f(0, 0, 8, inferop_amd.dtype.bf16, 4, 256) == S.ERR_ARGUMENT
+    h = inferop_amd.fused_add_rmsnorm_quant_fp8
+    assert h(0, 0, 0, 0, 0, inferop_amd.dtype.bf16, 4, 100) == S.ERR_SHAPE
+    assert h(0, 0, 0, 0, 0, inferop_amd.dtype.fp8_e4m3, 4, 128) == S.ERR_DTYPE
+    assert h(0, 0, 0, 0, 8, inferop_amd.dtype.bf16, 4, 128) == S.ERR_ARGUMENT
 
 
 def test_gemm_guards_print_reference_diagnostic(capfd):

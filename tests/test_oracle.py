@@ -288,3 +288,53 @@ def test_weight_block_quant_multiplies_by_reciprocal():
             assert bq[r, c] == L.orc_grid_encode(float(np.float32(v * inv))), (amax, v)
             differ += bq[r, c] != L.orc_grid_encode(float(np.float32(v / s)))
     assert differ >= len(pairs)
+
+
+@pytest.mark.skipif(not oracle.ref_available(), reason="reference build not present")
+def test_producers_bit_exact_vs_reference():
+    # reference.cpp:11-35, 55-64 compiled from the reference sources
+    import ctypes
+    R = oracle.ref()
+    g = np.random.default_rng(21)
+    gu = (3.0 * g.standard_normal((33, 2 * 384))).astype(np.float32)
+    gu[0, :8] = [0.0, -0.0, 88.0, -88.0, 100.0, -104.0, 1e-30, -1e-30]
+    want = np.empty((33, 384), np.float32)
+    R.ref_silu_and_mul(want.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                       gu.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), 33, 384)
+    got = oracle.silu_and_mul(gu)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    res = g.standard_normal((17, 1536)).astype(np.float32)
+    x = g.standard_normal((17, 1536)).astype(np.float32)
+    w = (1.0 + 0.1 * g.standard_normal(1536)).astype(np.float32)
+    r2, out = oracle.fused_add_rmsnorm(res, x, w, 1e-6)
+    rr = res.copy()
+    out_ref = np.empty_like(res)
+    fp = ctypes.POINTER(ctypes.c_float)
+    R.ref_fused_add_rmsnorm(rr.ctypes.data_as(fp), out_ref.ctypes.data_as(fp),
+                            x.ctypes.data_as(fp), w.ctypes.data_as(fp), 17, 1536, 1e-6)
+    assert np.array_equal(r2.view(np.uint32), rr.view(np.uint32))
+    assert np.array_equal(out.view(np.uint32), out_ref.view(np.uint32))
+    y = oracle.rmsnorm(x, w, 1e-5)
+    y_ref = np.empty_like(x)
+    R.ref_rmsnorm(y_ref.ctypes.data_as(fp), x.ctypes.data_as(fp), w.ctypes.data_as(fp), 17, 1536,
+                  1e-5)
+    assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32))
+
+
+def test_producers_closed_forms():
+    # SiLU within a few fp32 ulps of the float64 formula; RMSNorm exact on
+    # integer inputs (every product and partial sum is exact in fp32)
+    g = np.random.default_rng(22)
+    gu = (4.0 * g.standard_normal((8, 2 * 256))).astype(np.float32)
+    got = oracle.silu_and_mul(gu).astype(np.float64)
+    gg, uu = gu[:, :256].astype(np.float64), gu[:, 256:].astype(np.float64)
+    want = gg / (1.0 + np.exp(-gg)) * uu
+    assert (np.abs(got - want) <= 4 * np.spacing(np.abs(want).astype(np.float32)) + 1e-37).all()
+    res = g.integers(-8, 9, (4, 1024)).astype(np.float32)
+    x = g.integers(-8, 9, (4, 1024)).astype(np.float32)
+    w = g.integers(1, 4, 1024).astype(np.float32)
+    r2, out = oracle.fused_add_rmsnorm(res, x, w, 0.0)
+    assert np.array_equal(r2, res + x)
+    ss = (r2.astype(np.float64) ** 2).sum(axis=1, keepdims=True)
+    inv = np.float32(1) / np.sqrt((ss / 1024).astype(np.float32)).astype(np.float32)
+    assert np.array_equal(out, (r2 * inv) * w)
