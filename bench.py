@@ -379,6 +379,24 @@ def main():
         del res_, xs_, wn, fq, fs, gf
         result["fused_producers"] = {"shapes": fres, "peak_gbs": HBM_PEAK_GBS}
 
+        # ---------------- MoE routing: DeepSeek-V3 shape, 256 experts, top-8 ----------------
+        tres = []
+        for tok in (64, 4096):
+            lg = torch.randn((tok, 256), generator=gen, device=dev) * 2.0
+            tid = torch.empty((tok, 8), dtype=torch.int32, device=dev)
+            twt = torch.empty((tok, 8), dtype=torch.float32, device=dev)
+
+            def ftk(i, lg=lg, tid=tid, twt=twt, tok=tok):
+                st = ia.topk_softmax(tid, twt, lg, tok, 256, 8, True, sp)
+                assert st == 0, st
+
+            gt = capture(lambda: [ftk(i) for i in range(8)])
+            time_graphs([gt], 2)
+            us = time_graphs([gt], 5) / 8 * 1e3
+            tres.append({"tokens": tok, "experts": 256, "topk": 8, "us": round(us, 2)})
+            del lg, tid, twt, gt
+        result["topk_softmax"] = {"shapes": tres}
+
         result["quant"] = {"shapes": qres, "peak_gbs": HBM_PEAK_GBS,
                            "roofline": {"bound": "hbm", "kernel": "per-token-group quantizer",
                                         "achieved": qres[-1]["gbs"], "peak": HBM_PEAK_GBS,

@@ -60,6 +60,13 @@ int inferop_w8a8_block_fp8_gemm(void* c, const void* a_q, const void* a_scales, 
                                 int32_t group_size, int32_t block_n, int32_t out_dt,
                                 void* stream);
 
+/* --- replaces ops.h:108-110 topk_softmax ---
+ * tokens <= 0, num_experts <= 0, num_experts > 1024, topk <= 0 or
+ * topk > num_experts return INFEROP_ERR_SHAPE and write nothing (the
+ * reference's silent no-op).  renormalize: 0 or 1. */
+int inferop_topk_softmax(int32_t* topk_ids, void* topk_weights, const void* logits, int32_t tokens,
+                         int32_t num_experts, int32_t topk, int32_t renormalize, void* stream);
+
 /* --- extension: 128x128 weight block quantizer (no counterpart in the
  * reference ops.h; the recipe of its tests/test_gemm.cpp:28-45), see
  * inferop::quant_fp8_weight_block in ops.h.  group_size != 128,

@@ -4,7 +4,9 @@
 // function below has the reference's exact C++ signature and default arguments, so the
 // Itanium-mangled symbols exported by libinferop.so are the ones a program
 // built against the reference links to.  Only the FP8 path is provided
-// (quantizer, dequantizer, blockwise GEMM) plus device introspection, and
+// (quantizer, dequantizer, blockwise GEMM, and the MoE routing that selects
+// the experts whose FP8 weights a token multiplies) plus device
+// introspection, and
 // three extensions: the weight block quantizer the reference keeps in its
 // tests, and the two producers of the quantizer's input fused with it.
 //
@@ -58,6 +60,16 @@ void w8a8_block_fp8_gemm(void* c, const void* a_q, const void* a_scales, const v
                          const void* b_scales, int64_t m, int64_t n, int64_t k,
                          int group_size = 128, int block_n = 128, dtype out_dt = dtype::bf16,
                          void* stream = nullptr);
+
+// --- MoE routing (reference ops.h:102-110) ------------------------------------
+//   logits: [tokens, num_experts] fp32, num_experts <= 1024
+//   topk_ids: int32 [tokens, topk]; topk_weights: fp32 [tokens, topk]
+//   softmax over the experts, the topk most probable (lower index first on
+//   ties), weights = probability, divided by their sum when renormalize.
+// Invalid sizes (tokens, num_experts <= 0, num_experts > 1024, topk <= 0,
+// topk > num_experts) are silent no-ops.
+void topk_softmax(int32_t* topk_ids, void* topk_weights, const void* logits, int tokens,
+                  int num_experts, int topk, bool renormalize = true, void* stream = nullptr);
 
 // --- extension: 128x128 weight block quantization ----------------------------
 // No counterpart in the reference ops.h: the reference quantizes weights in

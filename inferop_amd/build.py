@@ -21,7 +21,7 @@ LIB = os.path.join(PKG, "libinferop.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CXX = os.environ.get("CXX", "g++")
 
-HIP_SOURCES = ["quant.hip", "gemm.hip", "device.hip"]
+HIP_SOURCES = ["quant.hip", "gemm.hip", "device.hip", "moe.hip"]
 CXX_SOURCES = ["ops.cpp"]
 
 HIP_FLAGS = [

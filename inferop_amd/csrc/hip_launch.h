@@ -39,6 +39,10 @@ int inferop_hip_add_rmsnorm_quant(void* residual, uint8_t* q, float* scales, con
                                   const void* weight, int32_t dt, int64_t rows, int64_t cols,
                                   float eps, void* stream);
 
+/* ---- MoE routing: softmax + top-k per token (num_experts <= 1024) ---- */
+int inferop_hip_topk_softmax(int32_t* ids, float* weights, const float* logits, int tokens,
+                             int num_experts, int topk, int renormalize, void* stream);
+
 /* ---- blockwise FP8 GEMM ----
  * cfg: index into the kernel table (inferop_hip_gemm_num_configs());
  * split_k: number of K partitions (1 = none); partitions > 1 reduce through

@@ -234,6 +234,17 @@ int rmsnorm_quant_impl(void* residual, void* q, void* scales, const void* x, con
                                                      rows, cols, eps, stream));
 }
 
+int topk_impl(int32_t* ids, void* weights, const void* logits, int32_t tokens, int32_t experts,
+              int32_t topk, int32_t renormalize, void* stream) {
+  // reference moe/topk_softmax.cu:104-108 guard
+  if (tokens <= 0 || experts <= 0 || experts > 1024 || topk <= 0 || topk > experts)
+    return INFEROP_ERR_SHAPE;
+  if (!current_device()) return INFEROP_ERR_DEVICE;
+  return status_of_hip(inferop_hip_topk_softmax(ids, static_cast<float*>(weights),
+                                                static_cast<const float*>(logits), tokens, experts,
+                                                topk, renormalize ? 1 : 0, stream));
+}
+
 bool gemm_shape_ok(int64_t m, int64_t n, int64_t k, int32_t group_size, int32_t block_n) {
   // reference w8a8_block_fp8.cu:167-173, including its diagnostic line.
   if (group_size != 128 || block_n != 128 || k % 128 != 0 || m <= 0 || n <= 0) {
@@ -320,6 +331,12 @@ void w8a8_block_fp8_gemm(void* c, const void* a_q, const void* a_scales, const v
                   int32_t(out_dt), stream);
 }
 
+void topk_softmax(int32_t* topk_ids, void* topk_weights, const void* logits, int tokens,
+                  int num_experts, int topk, bool renormalize, void* stream) {
+  (void)topk_impl(topk_ids, topk_weights, logits, tokens, num_experts, topk, renormalize ? 1 : 0,
+                  stream);
+}
+
 void quant_fp8_weight_block(void* b_q, void* b_scales, const void* w, dtype dt, int64_t n,
                             int64_t k, int group_size, int block_n, void* stream) {
   (void)weight_quant_impl(b_q, b_scales, w, int32_t(dt), n, k, group_size, block_n, stream);
@@ -376,6 +393,12 @@ extern "C" int inferop_w8a8_block_fp8_gemm(void* c, const void* a_q, const void*
                                            int64_t n, int64_t k, int32_t group_size,
                                            int32_t block_n, int32_t out_dt, void* stream) {
   return gemm_impl(c, a_q, a_scales, b_q, b_scales, m, n, k, group_size, block_n, out_dt, stream);
+}
+
+extern "C" int inferop_topk_softmax(int32_t* topk_ids, void* topk_weights, const void* logits,
+                                    int32_t tokens, int32_t num_experts, int32_t topk,
+                                    int32_t renormalize, void* stream) {
+  return topk_impl(topk_ids, topk_weights, logits, tokens, num_experts, topk, renormalize, stream);
 }
 
 extern "C" int inferop_quant_fp8_weight_block(void* b_q, void* b_scales, const void* w, int32_t dt,

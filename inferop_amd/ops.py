@@ -104,6 +104,13 @@ def w8a8_block_fp8_gemm(c, a_q, a_scales, b_q, b_scales, m: int, n: int, k: int,
         block_n, int(out_dt), _stream(stream))
 
 
+# ---- MoE routing (reference ops.h:102-110) ---------------------------------------
+def topk_softmax(topk_ids, topk_weights, logits, tokens: int, num_experts: int, topk: int,
+                 renormalize: bool = True, stream=None) -> int:
+    return lib().inferop_topk_softmax(_ptr(topk_ids), _ptr(topk_weights), _ptr(logits), tokens,
+                                      num_experts, topk, 1 if renormalize else 0, _stream(stream))
+
+
 # ---- extension: weight block quantizer (the reference's test recipe,
 # tests/test_gemm.cpp:28-45; no counterpart in its ops.h) ---------------------------
 def quant_fp8_weight_block(b_q, b_scales, w, dt, n: int, k: int, group_size: int = 128,

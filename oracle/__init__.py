@@ -72,6 +72,8 @@ def lib():
         L.orc_fused_add_rmsnorm.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64, _i64,
                                             ctypes.c_float]
         L.orc_silu_and_mul.argtypes = [_f32p, _f32p, _i64, _i64]
+        L.orc_topk_softmax.argtypes = [ctypes.POINTER(ctypes.c_int32), _f32p, _f32p, _i64, _i32,
+                                       _i32, _i32]
         L.orc_sweep_encode_vs_grid.restype = _u64
         L.orc_sweep_encode_vs_grid.argtypes = [_u64, _u64]
         L.orc_encode_checksum.restype = _u64
@@ -109,6 +111,8 @@ def ref():
         R.ref_fused_add_rmsnorm.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64, _i64,
                                             ctypes.c_float]
         R.ref_silu_and_mul.argtypes = [_f32p, _f32p, _i64, _i64]
+        R.ref_topk_softmax.argtypes = [ctypes.POINTER(ctypes.c_int32), _f32p, _f32p, _i64,
+                                       ctypes.c_int, ctypes.c_int, ctypes.c_int]
         _ref = R
     return _ref
 
@@ -233,3 +237,14 @@ def rmsnorm(x: np.ndarray, weight: np.ndarray, eps: float = 1e-6) -> np.ndarray:
     out = np.empty_like(xr)
     lib().orc_rmsnorm(_ptr(out, _f32p), _ptr(xr, _f32p), _ptr(w, _f32p), rows, cols, eps)
     return out
+
+
+def topk_softmax(logits: np.ndarray, topk: int, renormalize: bool = True):
+    """reference.cpp:152-181 -> (ids int32 [tokens, topk], weights fp32 [tokens, topk])."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    t, e = lg.shape
+    ids = np.empty((t, topk), np.int32)
+    w = np.empty((t, topk), np.float32)
+    lib().orc_topk_softmax(ids.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), _ptr(w, _f32p),
+                           _ptr(lg, _f32p), t, e, topk, 1 if renormalize else 0)
+    return ids, w

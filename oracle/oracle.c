@@ -301,6 +301,47 @@ void orc_silu_and_mul(float* out, const float* gate_up, int64_t tokens, int64_t 
   }
 }
 
+/* reference/reference.cpp:152-181.  The reference's std::stable_sort with
+ * the comparator (p[a] > p[b], then a < b) is restated as a stable insertion
+ * sort with the same comparator (the order is total for NaN-free logits, so
+ * any stable sort gives the same permutation). */
+void orc_topk_softmax(int32_t* topk_ids, float* topk_weights, const float* logits, int64_t tokens,
+                      int32_t num_experts, int32_t topk, int32_t renormalize) {
+  float probs[1024];
+  int order[1024];
+  for (int64_t t = 0; t < tokens; ++t) {
+    const float* row = logits + t * num_experts;
+    float mx = -INFINITY;
+    for (int e = 0; e < num_experts; ++e) mx = (mx < row[e]) ? row[e] : mx;
+    float l = 0.0f;
+    for (int e = 0; e < num_experts; ++e) {
+      probs[e] = expf(row[e] - mx);
+      l += probs[e];
+    }
+    for (int e = 0; e < num_experts; ++e) {
+      /* insert e after every element that precedes it */
+      int pos = e;
+      while (pos > 0) {
+        const int o = order[pos - 1];
+        const int before = (probs[e] != probs[o]) ? (probs[e] > probs[o]) : (e < o);
+        if (!before) break;
+        order[pos] = o;
+        --pos;
+      }
+      order[pos] = e;
+    }
+    float wsum = 0.0f;
+    for (int k = 0; k < topk; ++k) {
+      topk_ids[t * topk + k] = order[k];
+      topk_weights[t * topk + k] = probs[order[k]] / l;
+      wsum += probs[order[k]] / l;
+    }
+    if (renormalize && wsum > 0.0f) {
+      for (int k = 0; k < topk; ++k) topk_weights[t * topk + k] /= wsum;
+    }
+  }
+}
+
 /* ---- independent encoder: nearest OCP grid point ------------------------- */
 
 /* Positive finite E4M3 values, codes 0x00..0x7E, from the OCP definition

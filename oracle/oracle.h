@@ -58,6 +58,12 @@ void orc_fused_add_rmsnorm(float* residual, float* out, const float* x, const fl
 /* reference/reference.cpp:55-64: out[t, i] = silu(gate_up[t, i]) * gate_up[t, d + i]. */
 void orc_silu_and_mul(float* out, const float* gate_up, int64_t tokens, int64_t d);
 
+/* reference/reference.cpp:152-181: softmax over num_experts logits per token,
+ * experts stably sorted by probability descending (index ascending on ties),
+ * the first topk with weight p / l, renormalized by their sum on request. */
+void orc_topk_softmax(int32_t* topk_ids, float* topk_weights, const float* logits, int64_t tokens,
+                      int32_t num_experts, int32_t topk, int32_t renormalize);
+
 /* Independent E4M3 encoder: nearest point of the 253-value finite grid built
  * from the OCP definition, ties to the even encoding, |f| >= 448 saturates
  * (tests/test_fp8.cpp:8-50 describes the same oracle).  NaN -> sign|0x7F. */

@@ -70,4 +70,9 @@ void ref_silu_and_mul(float* out, const float* gate_up, int64_t tokens, int64_t 
   inferop::ref::silu_and_mul(out, gate_up, tokens, d);
 }
 
+void ref_topk_softmax(int32_t* ids, float* w, const float* logits, int64_t tokens, int experts,
+                      int topk, int renormalize) {
+  inferop::ref::topk_softmax(ids, w, logits, tokens, experts, topk, renormalize != 0);
+}
+
 }  // extern "C"

@@ -51,6 +51,7 @@ OPS_MANGLED = [
     "_ZN7inferop25quant_fp8_per_token_groupEPvS0_PKvNS_5dtypeElliS0_",
     "_ZN7inferop27dequant_fp8_per_token_groupEPvNS_5dtypeEPKvS3_lliS0_",
     "_ZN7inferop19w8a8_block_fp8_gemmEPvPKvS2_S2_S2_llliiNS_5dtypeES0_",
+    "_ZN7inferop12topk_softmaxEPiPvPKviiibS1_",
 ]
 
 
@@ -71,6 +72,7 @@ int main() {
   quant_fp8_per_token_group(nullptr, nullptr, nullptr, dtype::bf16, 4, 100, 128);
   w8a8_block_fp8_gemm(nullptr, nullptr, nullptr, nullptr, nullptr, 4, 8, 100);
   if (false) {
+    topk_softmax(nullptr, nullptr, nullptr, 1, 8, 2);
     dequant_fp8_per_token_group(nullptr, dtype::bf16, nullptr, nullptr, 1, 128);
     w8a8_block_fp8_gemm(nullptr, nullptr, nullptr, nullptr, nullptr, 1, 1, 128, 128, 128,
                         dtype::fp16, nullptr);
@@ -132,6 +134,10 @@ def test_quant_guards_without_touching_memory():
     assert f(0, 0, 0, inferop_amd.dtype.bf16, 4, 256, group_size=64) == S.ERR_SHAPE
     assert f(0, 0, 0, inferop_amd.dtype.fp8_e4m3, 4, 256) == S.ERR_DTYPE
     assert f(0, 0, 8, inferop_amd.dtype.bf16, 4, 256) == S.ERR_ARGUMENT
+    t = inferop_amd.topk_softmax
+    assert t(0, 0, 0, 4, 1025, 2) == S.ERR_SHAPE
+    assert t(0, 0, 0, 4, 8, 9) == S.ERR_SHAPE
+    assert t(0, 0, 0, 0, 8, 2) == S.ERR_SHAPE
     h = inferop_amd.fused_add_rmsnorm_quant_fp8
     assert h(0, 0, 0, 0, 0, inferop_amd.dtype.bf16, 4, 100) == S.ERR_SHAPE
     assert h(0, 0, 0, 0, 0, inferop_amd.dtype.fp8_e4m3, 4, 128) == S.ERR_DTYPE

@@ -338,3 +338,53 @@ def test_producers_closed_forms():
     ss = (r2.astype(np.float64) ** 2).sum(axis=1, keepdims=True)
     inv = np.float32(1) / np.sqrt((ss / 1024).astype(np.float32)).astype(np.float32)
     assert np.array_equal(out, (r2 * inv) * w)
+
+
+def _topk_cases():
+    g = np.random.default_rng(51)
+    yield (2.0 * g.standard_normal((257, 256))).astype(np.float32), 8
+    yield (2.0 * g.standard_normal((3, 8))).astype(np.float32), 2
+    yield (2.0 * g.standard_normal((17, 1024))).astype(np.float32), 16
+    tie = np.zeros((4, 64), np.float32)          # all equal: index order
+    tie[1, 10] = tie[1, 20] = 1.0                # equal maxima
+    tie[2] = np.round(g.standard_normal(64))     # many exact ties
+    tie[3, :] = -120.0                           # probabilities that underflow together
+    tie[3, 5] = 0.0
+    yield tie, 6
+
+
+@pytest.mark.skipif(not oracle.ref_available(), reason="reference build not present")
+def test_topk_softmax_bit_exact_vs_reference():
+    import ctypes
+    R = oracle.ref()
+    for lg, k in _topk_cases():
+        for renorm in (True, False):
+            ids, w = oracle.topk_softmax(lg, k, renorm)
+            t, e = lg.shape
+            ids_r = np.empty((t, k), np.int32)
+            w_r = np.empty((t, k), np.float32)
+            R.ref_topk_softmax(ids_r.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+                               w_r.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                               np.ascontiguousarray(lg).ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                               t, e, k, int(renorm))
+            assert np.array_equal(ids, ids_r)
+            assert np.array_equal(w.view(np.uint32), w_r.view(np.uint32))
+
+
+def test_topk_softmax_closed_form():
+    # tests/test_topk.cpp:13-34 properties, and the float64 softmax order
+    for lg, k in _topk_cases():
+        ids, w = oracle.topk_softmax(lg, k, True)
+        assert np.allclose(w.sum(axis=1), 1.0, atol=1e-5)
+        assert (np.diff(w, axis=1) <= 0).all()
+        assert all(len(set(r)) == k for r in ids)
+        p = np.exp(lg.astype(np.float64) - lg.max(axis=1, keepdims=True))
+        for r in range(lg.shape[0]):
+            # float64 order with index tie-break agrees wherever fp32 keeps values apart
+            o = sorted(range(lg.shape[1]), key=lambda e: (-p[r, e], e))[:k]
+            pf = np.float32(p[r])
+            if len(set(pf[o].tolist())) == k and len(np.unique(pf)) == lg.shape[1]:
+                assert list(ids[r]) == o
+        _, w0 = oracle.topk_softmax(lg, k, False)
+        l = np.exp(lg.astype(np.float64) - lg.max(axis=1, keepdims=True)).sum(axis=1, keepdims=True)
+        assert np.allclose(w0, np.sort(p / l, axis=1)[:, ::-1][:, :k], rtol=1e-5, atol=1e-9)
