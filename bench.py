@@ -37,6 +37,9 @@ DECODE_NK = ((7168, 2048), (4096, 7168), (2112, 7168))
 PREFILL_NK = ((24576, 1536), (32768, 512), (7168, 16384), (4608, 7168))
 QUANT_SHAPES = ((4096, 7168), (4096, 16384), (8192, 18432))
 PER_KERNEL_LAUNCHES = 20
+# prefill GEMMs per captured graph: back-to-back launches in steady state (with
+# a handful per graph the replay boundaries add tens of microseconds a launch)
+PREFILL_LAUNCHES = 20
 # HBM bytes per decode-GEMM launch, mean over the 9 decode shapes: FETCH_SIZE +
 # WRITE_SIZE from rocprofv3 runs of `bench.py --traffic-pass`, each scaled by
 # what the counter reads for a 256 MiB streaming kernel in the same process
@@ -263,9 +266,9 @@ def main():
                 st = ia.w8a8_block_fp8_gemm(c, q, s, bq, bs, m, n, k, 128, 128, DT.bf16, sp)
                 assert st == 0, st
 
-            gg = capture(lambda: [g(i) for i in range(4)])
+            gg = capture(lambda: [g(i) for i in range(PREFILL_LAUNCHES)])
             time_graphs([gg], 2)
-            us = time_graphs([gg], 5) / 4 * 1e3
+            us = time_graphs([gg], 5) / PREFILL_LAUNCHES * 1e3
             tflops = 2.0 * m * n * k / (us * 1e-6) / 1e12
             ai = 2.0 * m * n * k / gemm_bytes(m, n, k)
             bound = min(FP8_PEAK_TFLOPS, ai * HBM_PEAK_GBS / 1e3)

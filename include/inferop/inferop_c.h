@@ -90,7 +90,9 @@ int inferop_fused_add_rmsnorm_quant_fp8(void* residual, void* q, void* scales, c
 
 /* --- tuning and testing (no counterpart in the reference) ---
  * The GEMM with an explicit kernel configuration and split-K factor instead
- * of the automatic gfx950 choice.  config in [0, inferop_gemm_num_configs()). */
+ * of the automatic gfx950 choice.  config in [0, inferop_gemm_num_configs()).
+ * The persistent configurations ("per_" names) take whole tiles (split_k is
+ * ignored) and need an even K / 128; other K return INFEROP_ERR_ARGUMENT. */
 int inferop_gemm_num_configs(void);
 const char* inferop_gemm_config_name(int config);
 int inferop_w8a8_block_fp8_gemm_config(void* c, const void* a_q, const void* a_scales,

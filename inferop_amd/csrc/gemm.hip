@@ -18,7 +18,7 @@
 // 16-byte chunks (l / 16) and (l / 16 + 4) of the 128-byte group.  Both
 // operands use the same chunk order, so the K permutation cancels.
 //
-// Two kernel families:
+// Three kernel families:
 //
 // * decode (M <= 64 per tile, HBM-bound): no barrier in the main loop.  Each
 //   wave streams its 16 weight rows, U scale groups at a time, with direct
@@ -38,7 +38,15 @@
 //   chunk ^ (row & 7): the eight lanes of a ds_read_b128 phase hit eight
 //   different bank groups.  Tiles are renumbered so each XCD works on a
 //   contiguous, M-grouped range of tiles (L2 reuse of A and B).
+//
+// * persistent prefill (large M, whole tiles): the same stage layout and
+//   MFMA core in one workgroup per CU that walks its tiles without stopping
+//   the pipeline between them; half the waves issue the stage loads and the
+//   other half the output stores, so the stores of one tile drain while the
+//   next is multiplied.
+#include <atomic>
 #include <mutex>
+#include <type_traits>
 #include <unordered_map>
 
 #include "device_common.h"
@@ -653,12 +661,328 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_prefill_kernel(GemmArgs a) 
   }
 }
 
+// ---- persistent prefill kernel with load and store roles ---------------------------
+// grid: P workgroups (one per CU, two for 128x128 tiles).  Workgroup b walks
+// the output tiles u = lb, lb + P, lb + 2P, ... with lb its XCD-contiguous
+// number, so in every round the P tiles in flight are consecutive and each XCD
+// owns a contiguous, M-grouped block of them.  Requires an even number of
+// scale groups, so group g of any tile lives in stage buffer g % 2.
+//
+// The first half of the waves issue every direct-to-LDS stage load and the
+// second half every global store of the output.  A wave's vector memory
+// counter counts loads and stores in issue order, so a wave that waits for its
+// stage loads would also wait for any store it issued earlier; with the roles
+// split, the loading waves never have stores outstanding and the storing
+// waves never wait on the counter, and a tile's stores drain while the next
+// tiles are multiplied.  All waves multiply.  Across tiles the pipeline does
+// not stop: the next tile's first group streams in while the last group of
+// the current one is multiplied, and the output tile is staged through the
+// just-consumed stage buffer in passes of RP rows, which the storing waves
+// read into registers and store without waiting for the stores.
+//
+// The loads are inline assembly (see asm_buffer_to_lds16) and the loading
+// waves spread a stage's loads over the weight slices of the group being
+// multiplied, so issuing them does not hold back that wave's MFMAs.
+
+// Direct-to-LDS loads as inline assembly, for a kernel whose every wait on
+// them is an explicit stage barrier: the compiler's wait analysis does not see
+// these loads, so it never puts its own vmcnt waits in front of LDS reads or
+// barriers on their account (it does wherever its LDS alias information is
+// incomplete, and on a wave with global stores in flight such a wait would
+// stall on the stores).  M0 carries the wave's LDS destination.  The compiler
+// does not resolve hazards for inline assembly, so each load starts with five
+// wait states: enough for an SGPR operand (buffer resource or offset) written
+// by a VALU instruction such as v_readfirstlane, and for the M0 write ahead of
+// an LDS DMA.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+__device__ __forceinline__ void asm_buffer_to_lds16(const u32x4& rsrc, uint32_t lds, int voffset,
+                                                    int soffset) {
+  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :
+               : "v"(voffset), "s"(rsrc), "s"(soffset), "{m0}"(lds)
+               : "memory");
+}
+__device__ __forceinline__ void asm_global_to_lds4(const void* p, uint32_t lds) {
+  asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, off" : : "v"(p), "{m0}"(lds) : "memory");
+}
+// Raw buffer resource words (the fields make_rsrc sets) in SGPRs, for the
+// inline-assembly loads.
+__device__ __forceinline__ u32x4 rsrc_words(const void* base, uint32_t bytes) {
+  const uint64_t b = (uint64_t)(uintptr_t)base;
+  return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b),
+               (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32)),
+               (uint32_t)__builtin_amdgcn_readfirstlane((int)bytes), 0x00020000u};
+}
+
+// Largest bm / 2^i that fits in `fit` rows (the C tile leaves in equal passes).
+__host__ __device__ constexpr int pass_rows(int bm, int fit) {
+  return (bm <= fit || bm <= 16) ? bm : pass_rows(bm / 2, fit);
+}
+
+template <int BN, int BM, int WN, int WM, int OUT_DT>
+__global__ __launch_bounds__(64 * WN * WM) void gemm_persist_kernel(GemmArgs a) {
+  using OT = typename OutT<OUT_DT>::T;
+  constexpr int NW = WN * WM;
+  constexpr int NL = NW / 2;  // loading waves 0 .. NL-1, storing waves NL .. NW-1
+  constexpr int NS = NW - NL;
+  constexpr int TN = BN / WN, TM = BM / WM;
+  constexpr int SN = TN / 16, SM = TM / 16;
+  constexpr int kOffA = BN * 128;
+  constexpr int kOffSA = (BN + BM) * 128;
+  constexpr int kSaBlocks = (BM + 63) / 64;  // 64-row blocks of activation scales
+  constexpr int kOffSB = kOffSA + kSaBlocks * 256;
+  constexpr int kStage = ((kOffSB + 256) + 1023) / 1024 * 1024;
+  constexpr int RB = BN / 8 / NL;  // weight row blocks per loading wave per stage
+  constexpr int RA = BM / 8 / NL;  // activation row blocks per loading wave per stage
+  constexpr int kLoads = 2 + RB + RA;  // per loading wave per stage
+  constexpr int kPerSlice = (kLoads + SN - 2) / (SN - 1);
+  constexpr int kOB = (int)sizeof(OT);
+  constexpr int kRow = BN * kOB + (kOB == 2 ? 8 : 16);  // padded C row in LDS
+  constexpr int RP = pass_rows(BM, kStage / kRow);       // C rows per pass
+  constexpr int kChunks = BN * kOB / 16;                 // 16-byte pieces per C row
+  constexpr int kPieces = RP * kChunks / (64 * NS);      // per storing lane per pass
+  static_assert(NW % 2 == 0, "even wave count");
+  static_assert(TN % 16 == 0 && TM % 16 == 0 && SN >= 2, "wave tile of 16-row slices");
+  static_assert(128 % TN == 0, "a wave must stay inside one 128-row weight block");
+  static_assert(BN >= 128 ? BN % 128 == 0 : 128 % BN == 0, "tiles align to weight blocks");
+  static_assert(BN % (8 * NL) == 0 && BM % (8 * NL) == 0, "row blocks split over the loaders");
+  static_assert(BM % 64 == 0 && kSaBlocks <= NL, "one activation-scale block per loader");
+  static_assert(RP % 16 == 0 && BM % RP == 0, "C passes cover whole 16-row slices");
+  static_assert((RP * kChunks) % (64 * NS) == 0, "C pass splits over the storers");
+
+  __shared__ __attribute__((aligned(1024))) uint8_t smem0[kStage];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem1[kStage];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wn = wave % WN, wm = wave / WN;
+  const int M = a.m, N = a.n, K = a.k;
+  const int KG = K >> 7;
+  const int NB = (N + 127) >> 7;
+  const int tiles_n = (N + BN - 1) / BN, tiles_m = (M + BM - 1) / BM;
+  const int tiles = tiles_n * tiles_m;
+  const int P = gridDim.x;
+  int u = xcd_contiguous((int)blockIdx.x, P);
+  if (u >= tiles) return;
+
+  const int lrow = lane >> 3;
+  const int loff = lrow * K + ((lane & 7) ^ lrow) * 16;
+  const int rsub = lane & 15, c0 = lane >> 4;
+
+  f32x4 acc[SN][SM];
+  // one scale group from stage buffer st; between(i) runs after the MFMAs of
+  // weight slice i
+  auto compute = [&](const uint8_t* st, auto between) {
+    const uint8_t* bB = st;
+    const uint8_t* bA = st + kOffA;
+    const float* sA = reinterpret_cast<const float*>(st + kOffSA);
+    const float sbC = reinterpret_cast<const float*>(st + kOffSB)[(wn * TN) >> 7];
+    i32x8 aop[SM];
+#pragma unroll
+    for (int j = 0; j < SM; ++j) aop[j] = lds_operand(bA, wm * TM + 16 * j + rsub, c0);
+    float sab[SM];
+#pragma unroll
+    for (int j = 0; j < SM; ++j) sab[j] = sA[wm * TM + 16 * j + rsub] * sbC;
+    constexpr int PJ = SM >= 4 ? 2 : SM;
+#pragma unroll
+    for (int i = 0; i < SN; ++i) {
+      const i32x8 bop = lds_operand(bB, wn * TN + 16 * i + rsub, c0);
+#pragma unroll
+      for (int j0 = 0; j0 < SM; j0 += PJ) {
+        f32x4 pv[PJ];
+#pragma unroll
+        for (int j = 0; j < PJ; ++j) pv[j] = mfma_group(bop, aop[j0 + j]);
+#pragma unroll
+        for (int j = 0; j < PJ; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            acc[i][j0 + j][r] = __builtin_fmaf(pv[j][r], sab[j0 + j], acc[i][j0 + j][r]);
+      }
+      between(i);
+    }
+  };
+  // Keep a group's MFMAs ahead of the next barrier: otherwise the compiler
+  // may sink them next to the following group's operand reads and spill.
+  auto pin_acc = [&]() {
+#pragma unroll
+    for (int i = 0; i < SN; ++i)
+#pragma unroll
+      for (int j = 0; j < SM; ++j) asm volatile("" : "+v"(acc[i][j]));
+  };
+
+  // The roles run separate copies of the loop, so the compiler's own wait
+  // analysis never sees a load on a storing wave's path or a store on a
+  // loading wave's path.
+  auto run = [&](auto role) {
+    constexpr bool kLoader = decltype(role)::value;
+    // loading waves wait for their loads; storing waves have none
+    auto barrier = [&]() {
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm(kLoader ? 0 : 63));
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    };
+    const int l = kLoader ? wave : 0;
+    u32x4 rB = u32x4{0u, 0u, 0u, 0u}, rA = u32x4{0u, 0u, 0u, 0u};
+    const float* sa_src = a.as;
+    const float* sb_src = a.bs;
+    // tile buffers: rows past the last row of A or B read as zeros
+    auto set_loads = [&](int n0, int m0) {
+      if constexpr (kLoader) {
+        const int nrows = min(BN, N - n0), mrows = min(BM, M - m0);
+        rB = rsrc_words(a.bq + (int64_t)n0 * K, (uint32_t)(nrows * K));
+        rA = rsrc_words(a.aq + (int64_t)m0 * K, (uint32_t)(mrows * K));
+        sa_src = a.as + (int64_t)(m0 + min(min(l, kSaBlocks - 1) * 64 + lane, M - 1 - m0)) * KG;
+        constexpr int kSbBlocks = BN >= 128 ? BN / 128 : 1;
+        const int nb = min((n0 >> 7) + min(lane, kSbBlocks - 1), NB - 1);
+        sb_src = a.bs + (int64_t)nb * KG;
+      }
+    };
+    // Load d of a stage: 0 the activation scales, 1 the weight scales, then
+    // RB weight and RA activation row blocks.  Every loader issues the same
+    // loads (loaders past the last activation-scale block repeat it, and all
+    // write the same weight scales), which the stage barrier's count assumes.
+    auto issue_load = [&](int g, uint8_t* sb, int d) {
+      if constexpr (kLoader) {
+        const uint32_t base = lds_addr(sb);
+        if (d == 0) {
+          asm_global_to_lds4(sa_src + g, base + kOffSA + min(l, kSaBlocks - 1) * 256);
+        } else if (d == 1) {
+          asm_global_to_lds4(sb_src + g, base + kOffSB);
+        } else if (d < 2 + RB) {
+          const int r = d - 2;
+          asm_buffer_to_lds16(rB, base + 8 * (l + r * NL) * 128, loff,
+                              8 * (l + r * NL) * K + g * 128);
+        } else {
+          const int r = d - 2 - RB;
+          asm_buffer_to_lds16(rA, base + kOffA + 8 * (l + r * NL) * 128, loff,
+                              8 * (l + r * NL) * K + g * 128);
+        }
+      }
+    };
+    // stage g's loads, kPerSlice after each of the first weight slices
+    auto spread = [&](int g, uint8_t* sb) {
+      return [&, g, sb](int i) {
+#pragma unroll
+        for (int q = 0; q < kPerSlice; ++q)
+          if (i * kPerSlice + q < kLoads) issue_load(g, sb, i * kPerSlice + q);
+      };
+    };
+
+    int tn, tm;
+    tile_of(u, tiles_n, tiles_m, &tn, &tm);
+    int n0 = tn * BN, m0 = tm * BM;
+    set_loads(n0, m0);
+#pragma unroll
+    for (int d = 0; d < kLoads; ++d) issue_load(0, smem0, d);
+    barrier();
+    for (;;) {
+      const int nu = u + P;
+      const bool has_next = nu < tiles;
+      int nn0 = n0, nm0 = m0;
+      if (has_next) {
+        int ntn, ntm;
+        tile_of(nu, tiles_n, tiles_m, &ntn, &ntm);
+        nn0 = ntn * BN;
+        nm0 = ntm * BM;
+      }
+#pragma unroll
+      for (int i = 0; i < SN; ++i)
+#pragma unroll
+        for (int j = 0; j < SM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      // on entry group 0 of the tile is in buffer 0
+      for (int g0 = 0; g0 + 2 < KG; g0 += 2) {
+        compute(smem0, spread(g0 + 1, smem1));
+        pin_acc();
+        barrier();  // group g0 + 1 landed; every wave is done with buffer 0
+        compute(smem1, spread(g0 + 2, smem0));
+        pin_acc();
+        barrier();  // group g0 + 2 landed; every wave is done with buffer 1
+      }
+      compute(smem0, spread(KG - 1, smem1));
+      pin_acc();
+      barrier();  // group KG - 1 landed; every wave is done with buffer 0
+      // the next tile's first group (the last tile reloads its own, which
+      // keeps the group free of branches)
+      set_loads(nn0, nm0);
+      compute(smem1, spread(0, smem0));
+      pin_acc();
+      barrier();  // the next tile's group 0 landed; buffer 1 is free
+
+      // the output tile leaves through buffer 1, RP rows per pass
+      OT* C = reinterpret_cast<OT*>(a.c);
+      const bool vec = a.vec_ok && (N % (16 / kOB)) == 0;
+#pragma unroll
+      for (int p = 0; p < BM / RP; ++p) {
+#pragma unroll
+        for (int j = 0; j < SM; ++j) {
+          const int sr = wm * TM + 16 * j;  // first tile row of the slice
+          if (sr < p * RP || sr >= (p + 1) * RP) continue;
+#pragma unroll
+          for (int i = 0; i < SN; ++i) {
+            const int nl = wn * TN + 16 * i + 4 * c0;
+            uint8_t* dst = smem1 + (sr - p * RP + rsub) * kRow + nl * kOB;
+            if constexpr (kOB == 4) {
+              *reinterpret_cast<f32x4*>(dst) = acc[i][j];
+            } else {
+              typedef OT ot4 __attribute__((ext_vector_type(4)));
+              *reinterpret_cast<ot4*>(dst) =
+                  ot4{(OT)acc[i][j][0], (OT)acc[i][j][1], (OT)acc[i][j][2], (OT)acc[i][j][3]};
+            }
+          }
+        }
+        barrier();  // the pass is in LDS
+        if constexpr (!kLoader) {
+          // four pieces at a time: the accumulators of later passes are live
+          constexpr int QB = kPieces < 4 ? kPieces : 4;
+          static_assert(kPieces % QB == 0, "C pieces in batches");
+#pragma unroll
+          for (int q0 = 0; q0 < kPieces; q0 += QB) {
+            u32x4 piece[QB];
+#pragma unroll
+            for (int q = 0; q < QB; ++q) {
+              const int idx = (wave - NL) * 64 + lane + (q0 + q) * 64 * NS;
+              piece[q] = *reinterpret_cast<const u32x4*>(smem1 + (idx / kChunks) * kRow +
+                                                         (idx % kChunks) * 16);
+            }
+#pragma unroll
+            for (int q = 0; q < QB; ++q) {
+              const int idx = (wave - NL) * 64 + lane + (q0 + q) * 64 * NS;
+              const int m = m0 + p * RP + idx / kChunks, n = n0 + (idx % kChunks) * (16 / kOB);
+              if (m >= M || n >= N) continue;
+              OT* dst = C + (int64_t)m * N + n;
+              if (vec && n + 16 / kOB - 1 < N) {
+                __builtin_nontemporal_store(piece[q], reinterpret_cast<u32x4*>(dst));
+              } else {
+                const OT* e = reinterpret_cast<const OT*>(&piece[q]);
+                for (int r = 0; r < 16 / kOB && n + r < N; ++r) dst[r] = e[r];
+              }
+            }
+          }
+        }
+        barrier();  // the storing waves have read the pass out of LDS
+      }
+      if (!has_next) break;
+      u = nu;
+      n0 = nn0;
+      m0 = nm0;
+    }
+  };
+  if (wave < NL) {
+    run(std::integral_constant<bool, true>{});
+  } else {
+    run(std::integral_constant<bool, false>{});
+  }
+}
+
 // ---- kernel table -------------------------------------------------------------
 
 using KernelFn = void (*)(GemmArgs);
 
 struct CfgEntry {
-  int kind;  // 1 = decode, 2 = prefill
+  int kind;  // 1 = decode, 2 = prefill, 3 = persistent prefill
   int bn, bm, waves;
   const char* name;
   KernelFn fn[3];  // [out_dt index]
@@ -677,6 +1001,11 @@ struct CfgEntry {
    {gemm_prefill_kernel<BN, BM, WN, WM, ST, kFp32>,                                            \
     gemm_prefill_kernel<BN, BM, WN, WM, ST, kFp16>,                                            \
     gemm_prefill_kernel<BN, BM, WN, WM, ST, kBf16>}}
+
+#define PERSIST_CFG(BN, BM, WN, WM, NAME)                                                      \
+  {3, BN, BM, WN * WM, NAME,                                                                   \
+   {gemm_persist_kernel<BN, BM, WN, WM, kFp32>, gemm_persist_kernel<BN, BM, WN, WM, kFp16>,     \
+    gemm_persist_kernel<BN, BM, WN, WM, kBf16>}}
 
 const CfgEntry kCfgs[] = {
     DECODE_CFG(1, 1, 8, "dec_m16_k1_u8"),
@@ -698,6 +1027,9 @@ const CfgEntry kCfgs[] = {
     DECODE_LDS_CFG(2, 4, "decl_k2_u4"),
     DECODE_LDS_CFG(4, 4, "decl_k4_u4"),
     DECODE_LDS_CFG(8, 4, "decl_k8_u4"),
+    PERSIST_CFG(256, 256, 2, 4, "per_n256_m256_w8"),
+    PERSIST_CFG(256, 128, 4, 2, "per_n256_m128_w8"),
+    PERSIST_CFG(128, 128, 2, 2, "per_n128_m128_w4"),
 };
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
@@ -761,6 +1093,25 @@ hipError_t get_workspace(hipStream_t st, size_t partial_bytes, size_t counters, 
   return hipSuccess;
 }
 
+// Compute units of the current device (cached per device ordinal).
+hipError_t device_cus(int* cus) {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev >= 0 && dev < 64 && cached[dev].load(std::memory_order_relaxed) > 0) {
+    *cus = cached[dev].load(std::memory_order_relaxed);
+    return hipSuccess;
+  }
+  int v = 0;
+  e = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return e;
+  if (v <= 0) return hipErrorInvalidDevice;
+  if (dev >= 0 && dev < 64) cached[dev].store(v, std::memory_order_relaxed);
+  *cus = v;
+  return hipSuccess;
+}
+
 int dt_index(int32_t out_dt) {
   switch (out_dt) {
     case kFp32: return 0;
@@ -818,6 +1169,18 @@ extern "C" int inferop_hip_gemm_w8a8_block(void* c, const uint8_t* a_q, const fl
     }
     hipLaunchKernelGGL(cf.fn[di], dim3((unsigned)tn, (unsigned)split, (unsigned)tm),
                        dim3(64 * cf.waves), 0, st, args);
+  } else if (cf.kind == 3) {
+    // persistent: whole tiles (split_k is ignored), an even number of scale
+    // groups, one workgroup per CU (two for 128x128 tiles, whose LDS allows it)
+    const int64_t tiles = tn * tm;
+    if (tiles > 0x7FFFFFFF || kg % 2 != 0) return hipErrorInvalidValue;
+    if ((int64_t)(cf.bn > cf.bm ? cf.bn : cf.bm) * k > 0x7FFFFFFF) return hipErrorInvalidValue;
+    int cus = 0;
+    hipError_t e = device_cus(&cus);
+    if (e != hipSuccess) return e;
+    const int64_t slots = (int64_t)cus * (cf.bn * cf.bm <= 128 * 128 ? 2 : 1);
+    const int64_t grid = tiles < slots ? tiles : slots;
+    hipLaunchKernelGGL(cf.fn[di], dim3((unsigned)grid), dim3(64 * cf.waves), 0, st, args);
   } else {
     const int64_t tiles = tn * tm;
     int split = launch->split_k < 1 ? 1 : launch->split_k;

@@ -56,7 +56,8 @@ typedef struct {
   int32_t bn;     /* block tile along N */
   int32_t bm;     /* block tile along M */
   int32_t waves;  /* waves per workgroup */
-  int32_t kind;   /* 1 = decode (16-row weight stripes), 2 = LDS-staged output tiles */
+  int32_t kind;   /* 1 = decode (16-row weight stripes), 2 = LDS-staged output tiles,
+                     3 = persistent LDS-staged tiles (split_k ignored, K/128 even) */
   const char* name;
 } inferop_gemm_cfg_info;
 

@@ -82,6 +82,9 @@ enum GemmCfg : int32_t {
   kDecLdsK2 = 16,
   kDecLdsK4 = 17,
   kDecLdsK8 = 18,
+  kPerN256M256 = 19,
+  kPerN256M128 = 20,
+  kPerN128M128 = 21,
 };
 
 struct GemmChoice {
@@ -151,12 +154,15 @@ GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
   }
   // MFMA-bound: a 256x256 tile runs alone on a CU and does four 128x128
   // tiles' work in about 1.5x their time (two 128x128 tiles share a CU).
-  // Count whole rounds of workgroups for both and take the cheaper one.
+  // Count whole rounds of workgroups for both and take the cheaper one.  The
+  // 256x256 tiles run on the persistent kernel when K has an even number of
+  // scale groups (it keeps the pipeline going across a CU's tiles and drains
+  // their stores in the background).
   const int64_t t256 = ((n + 255) / 256) * ((m + 255) / 256);
   const int64_t t128 = ((n + 127) / 128) * ((m + 127) / 128);
   const int64_t r256 = (t256 + cus - 1) / cus;
   const int64_t r128 = (t128 + 2 * cus - 1) / (2 * cus);
-  if (2 * r256 * 3 < 2 * 2 * r128) return {kPreN256M256S2, 1};
+  if (2 * r256 * 3 < 2 * 2 * r128) return {kg % 2 == 0 ? kPerN256M256 : kPreN256M256S2, 1};
   // too few 128x128 tiles to fill the CUs: split K across workgroups, each
   // split keeping at least 16 scale groups (below that the fp32 partial
   // round trip costs more than the idle CUs) and at most four splits.
@@ -437,6 +443,10 @@ extern "C" int inferop_w8a8_block_fp8_gemm_config(void* c, const void* a_q, cons
   if (!valid_input_dtype(out_dt)) return INFEROP_ERR_DTYPE;
   if (config < 0 || config >= inferop_hip_gemm_num_configs() || split_k < 1)
     return INFEROP_ERR_ARGUMENT;
+  // the persistent kernels take an even number of scale groups
+  inferop_gemm_cfg_info info{};
+  if (inferop_hip_gemm_config_info(config, &info) != 0) return INFEROP_ERR_ARGUMENT;
+  if (info.kind == 3 && (k / 128) % 2 != 0) return INFEROP_ERR_ARGUMENT;
   if (!gemm_device()) return INFEROP_ERR_DEVICE;
   return gemm_launch(c, a_q, a_scales, b_q, b_scales, m, n, k, out_dt, config, split_k, stream);
 }

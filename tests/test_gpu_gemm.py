@@ -153,6 +153,32 @@ def test_every_kernel_config_ragged(config, split):
         assert_gemm_close(out_to_f32(c), want, f"cfg{config} split{split} {out}")
 
 
+def _cfg(name):
+    return next(i for i in range(N_CONFIGS) if inferop_amd.gemm_config_name(i) == name)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", ["per_n256_m256_w8", "per_n256_m128_w8", "per_n128_m128_w4"])
+def test_persistent_kernels_match_tiled_kernel(name):
+    # The persistent kernels walk several tiles per workgroup and keep the
+    # load pipeline running across tile boundaries; per output element they
+    # add the scale groups in the same order as the one-tile-per-workgroup
+    # kernel, so the outputs are identical, ragged edges included.  Shapes:
+    # many rounds of ragged tiles, the shortest K (two groups: no steady-state
+    # iteration), and fewer tiles than CUs.
+    device()
+    ref = _cfg("pre_n256_m256_w8_s2")
+    for (m, n, k) in [(4000, 9000, 512), (1500, 33000, 256), (700, 4100, 1536)]:
+        print(f"{name} {m}x{n}x{k}", flush=True)
+        a, aq, as_, bq, bs = _device_case(m, n, k, seed=m + n)
+        for out in ("bf16", "fp16", "fp32"):
+            want = _gemm(aq, as_, bq, bs, m, n, k, out, ref, 1)
+            got = _gemm(aq, as_, bq, bs, m, n, k, out, _cfg(name), 1)
+            assert torch.equal(got, want), f"{name} {m}x{n}x{k} {out}"
+        rows = np.unique(np.concatenate([[0, m - 1], np.random.default_rng(m).integers(0, m, 4)]))
+        _check_sampled(a, aq, as_, bq, bs, got, rows, f"{name} {m}x{n}x{k}")
+
+
 @pytest.mark.gpu
 def test_output_dtypes_and_odd_n():
     device()

@@ -173,6 +173,19 @@ def test_gemm_selection_covers_configs():
     # a long K over too few weight stripes to occupy every CU is split
     assert inferop_amd.gemm_select(1, 512, 8 * 7168)[1] > 1
     assert inferop_amd.gemm_select(1, 4096, 7168)[1] == 1
+    # 256x256 prefill tiles run on the persistent kernel when K / 128 is even,
+    # on the one-tile-per-workgroup kernel otherwise
+    assert names[inferop_amd.gemm_select(4096, 7168, 16384)[0]] == "per_n256_m256_w8"
+    assert names[inferop_amd.gemm_select(4096, 7168, 16384 + 128)[0]] == "pre_n256_m256_w8_s2"
+
+
+def test_persistent_config_rejects_odd_group_count():
+    # checked before any device work: the persistent kernels need K / 128 even
+    S = inferop_amd.Status
+    g = inferop_amd.w8a8_block_fp8_gemm_config
+    for i in range(inferop_amd.gemm_num_configs()):
+        if inferop_amd.gemm_config_name(i).startswith("per_"):
+            assert g(0, 0, 0, 0, 0, 256, 256, 384, inferop_amd.dtype.bf16, i, 1) == S.ERR_ARGUMENT
 
 
 @pytest.mark.skipif(shutil.which("nm") is None, reason="binutils missing")
