@@ -83,6 +83,42 @@ __device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t r, void* 
                                            voffset, soffset, 0, 0);
 }
 
+// Direct-to-LDS loads as inline assembly, for kernels that wait for them
+// explicitly (stage barriers, counted vmcnt waits): the compiler's wait analysis does not see
+// these loads, so it never puts its own vmcnt waits in front of LDS reads or
+// barriers on their account (it does wherever its LDS alias information is
+// incomplete, and on a wave with global stores in flight such a wait would
+// stall on the stores).  M0 carries the wave's LDS destination.  The compiler
+// does not resolve hazards for inline assembly, so each load starts with five
+// wait states: enough for an SGPR operand (buffer resource or offset) written
+// by a VALU instruction such as v_readfirstlane, and for the M0 write ahead of
+// an LDS DMA.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+__device__ __forceinline__ void asm_buffer_to_lds16(const u32x4& rsrc, uint32_t lds, int voffset,
+                                                    int soffset) {
+  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :
+               : "v"(voffset), "s"(rsrc), "s"(soffset), "{m0}"(lds)
+               : "memory");
+}
+__device__ __forceinline__ void asm_global_to_lds4(const void* p, uint32_t lds) {
+  asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, off" : : "v"(p), "{m0}"(lds) : "memory");
+}
+// Raw buffer resource words (the fields make_rsrc sets) in SGPRs, for the
+// inline-assembly loads.
+__device__ __forceinline__ u32x4 rsrc_words(const void* base, uint32_t bytes) {
+  const uint64_t b = (uint64_t)(uintptr_t)base;
+  return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b),
+               (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32)),
+               (uint32_t)__builtin_amdgcn_readfirstlane((int)bytes), 0x00020000u};
+}
+
+// s_waitcnt immediate (gfx9 encoding): at most n vector memory operations of
+// this wave outstanding and every LDS/scalar access completed.
+__device__ constexpr int vmcnt_lgkm0_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4); }
+
 __device__ __forceinline__ f32x4 mfma_group(const i32x8& w, const i32x8& x) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w, x, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0,
                                                           0, 127, 0, 127);
@@ -162,18 +198,63 @@ __device__ __forceinline__ bool splitk_fixup(const GemmArgs& a, f32x4 (&part)[LP
   }
   __syncthreads();
   if (!s_last) return false;
+  const float* base = a.ws + (int64_t)tile * tile_floats + (int64_t)pair_base * 256 + lane;
+  const int64_t split_floats = tiles * tile_floats;
+  if constexpr (LP > 8) {
+    // large tiles (never split by the automatic choice): one pair at a time,
+    // which keeps the kernel's register budget
 #pragma unroll
-  for (int q = 0; q < LP; ++q) {
-    if (!valid(q)) continue;
-    f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int zz = 0; zz < split; ++zz) {
-      const float* src = a.ws + ((int64_t)zz * tiles + tile) * tile_floats +
-                         (int64_t)pair_base * 256 + q * 256 + lane;
+    for (int q = 0; q < LP; ++q) {
+      if (!valid(q)) continue;
+      f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int zz = 0; zz < split; ++zz) {
+        const float* src = base + zz * split_floats + q * 256;
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        sum[r] += __hip_atomic_load(src + r * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int r = 0; r < 4; ++r)
+          sum[r] += __hip_atomic_load(src + r * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      part[q] = sum;
     }
-    part[q] = sum;
+  } else {
+    // The partials of ZB splits for QB pairs are loaded together before any
+    // is added, so the loads travel in parallel rather than one split at a
+    // time; each element still adds the splits in order 0, 1, ..., split - 1.
+    constexpr int QB = LP < 4 ? LP : 4;
+    constexpr int ZB = (LP <= 2 ? 16 : 8) / QB;
+    static_assert(LP % QB == 0, "pairs in whole batches");
+#pragma unroll
+    for (int q0 = 0; q0 < LP; q0 += QB) {
+      f32x4 sum[QB];
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) sum[qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int z0 = 0; z0 < split; z0 += ZB) {
+        f32x4 v[ZB][QB];
+#pragma unroll
+        for (int zb = 0; zb < ZB; ++zb) {
+          const int zz = min(z0 + zb, split - 1);  // past the last split: a harmless reload
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) {
+            if (!valid(q0 + qb)) continue;
+            const float* src = base + zz * split_floats + (q0 + qb) * 256;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              v[zb][qb][r] = __hip_atomic_load(src + r * 64, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+#pragma unroll
+        for (int zb = 0; zb < ZB; ++zb) {
+          if (z0 + zb >= split) break;
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sum[qb][r] += v[zb][qb][r];
+        }
+      }
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb)
+        if (valid(q0 + qb)) part[q0 + qb] = sum[qb];
+    }
   }
   if (threadIdx.x == 0)
     __hip_atomic_store(a.counters + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -388,6 +469,124 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_lds_kernel(GemmArgs a) {
   if (wk == 0) store_out4<OUT_DT>(a, m0 + rsub, n0 + 4 * c0, part[0]);
 }
 
+// ---- decode kernel for several activation tiles per weight stripe -------------------
+// grid: x = N stripes of 16 weight rows, y = M tiles of 16*MT rows.
+// A workgroup owns one 16-row weight stripe over the whole K range and MT
+// 16-row activation tiles; its WK waves split the scale groups and are summed
+// through LDS at the end (no split-K, so no round trip through device-coherent
+// partials).  Each weight byte leaves HBM once; the activations, shared by
+// every stripe, come from L2.  A wave streams its groups through two private
+// rings: UW weight slots (2 KB each), refilled UW groups ahead, so enough HBM
+// bytes are in flight to cover the latency, and UA activation slots (MT tiles,
+// their scales and the weight scale), refilled UA groups ahead from L2.
+// The loads are inline assembly issued in a fixed pattern, so a single
+// constant vmcnt wait covers the next group in every iteration (tail loads
+// re-read the last group into the slot just consumed).
+template <int MT, int WK, int UW, int UA, int OUT_DT>
+__global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
+  constexpr int kW = 2048;                          // 16 weight rows x 128 B
+  constexpr int kOffSa = MT * 2048;                 // in an activation slot
+  constexpr int kOffSb = kOffSa + 256;
+  constexpr int kA = MT * 2048 + 512;               // MT tiles + 64 sa + 64 sb
+  constexpr int kWave = UW * kW + UA * kA;
+  constexpr int kPerIter = 2 + 2 * MT + 2;          // loads issued per group
+  constexpr int kWait = (UA - 1) * kPerIter;        // loads that may stay in flight
+  static_assert(UW >= UA && UA >= 2 && kWait <= 63, "ring sizes");
+  static_assert(MT >= 1 && MT <= 4, "1 to 4 activation tiles");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[WK * kWave];
+
+  const int lane = threadIdx.x & 63;
+  const int wk = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int M = a.m, N = a.n, K = a.k;
+  const int KG = K >> 7;
+  const int NB = (N + 127) >> 7;
+  const int n0 = blockIdx.x * 16;
+  const int m0 = blockIdx.y * (16 * MT);
+  const int gw0 = wk * KG / WK, gw1 = (wk + 1) * KG / WK;
+  const int cnt = gw1 - gw0;
+  const int rsub = lane & 15, c0 = lane >> 4;
+  const int lrow = lane >> 3;
+  const int loff = lrow * K + ((lane & 7) ^ lrow) * 16;
+  uint8_t* const wave_lds = smem + wk * kWave;
+  const uint32_t wbase = lds_addr(wave_lds);
+  const uint32_t abase = wbase + UW * kW;
+
+  f32x4 acc[MT];
+#pragma unroll
+  for (int j = 0; j < MT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if (cnt > 0) {
+    // rows past the end of A or B read as zeros
+    const u32x4 rB = rsrc_words(a.bq + (int64_t)n0 * K, (uint32_t)(min(16, N - n0) * K));
+    const u32x4 rA = rsrc_words(a.aq + (int64_t)m0 * K, (uint32_t)(min(16 * MT, M - m0) * K));
+    const float* sa_src = a.as + (int64_t)(m0 + min(lane % (16 * MT), M - 1 - m0)) * KG;
+    const float* sb_src = a.bs + (int64_t)min(n0 >> 7, NB - 1) * KG;
+    auto issue_w = [&](int i) {  // group gw0 + i into weight slot i % UW
+      const int g = gw0 + min(i, cnt - 1);
+      const uint32_t dst = wbase + (uint32_t)(i % UW) * kW;
+      asm_buffer_to_lds16(rB, dst, loff, g * 128);
+      asm_buffer_to_lds16(rB, dst + 1024, loff, 8 * K + g * 128);
+    };
+    auto issue_a = [&](int i) {  // group gw0 + i into activation slot i % UA
+      const int g = gw0 + min(i, cnt - 1);
+      const uint32_t dst = abase + (uint32_t)(i % UA) * kA;
+#pragma unroll
+      for (int h = 0; h < 2 * MT; ++h) asm_buffer_to_lds16(rA, dst + h * 1024, loff, 8 * h * K + g * 128);
+      asm_global_to_lds4(sa_src + g, dst + kOffSa);
+      asm_global_to_lds4(sb_src + g, dst + kOffSb);
+    };
+    // Prologue in the loop's issue pattern: the weight slots beyond the
+    // activation depth first, then (weight, activation) pairs; after it, and
+    // after every iteration, exactly kWait loads follow the activations of the
+    // group consumed next.
+    for (int s = 0; s < UW - UA; ++s) issue_w(s);
+#pragma unroll
+    for (int j = 0; j < UA; ++j) {
+      issue_w(UW - UA + j);
+      issue_a(j);
+    }
+    for (int i = 0; i < cnt; ++i) {
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm(kWait));  // group i has landed
+      asm volatile("" ::: "memory");
+      const uint8_t* W = wave_lds + (i % UW) * kW;
+      const uint8_t* A = wave_lds + UW * kW + (i % UA) * kA;
+      const i32x8 wop = lds_operand(W, rsub, c0);
+      const float sb = reinterpret_cast<const float*>(A + kOffSb)[0];
+#pragma unroll
+      for (int j = 0; j < MT; ++j) {
+        const f32x4 pv = mfma_group(wop, lds_operand(A + j * 2048, rsub, c0));
+        const float sc = reinterpret_cast<const float*>(A + kOffSa)[16 * j + rsub] * sb;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[j][r] = __builtin_fmaf(pv[r], sc, acc[j][r]);
+      }
+      // the slots of group i are read (operands in registers) before refilling
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      issue_w(i + UW);
+      issue_a(i + UA);
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm(0));  // tail loads have landed
+  }
+
+  // sum the WK slices through LDS (the slots are free now); wave w adds up
+  // and stores tile w % MT
+  if constexpr (WK > 1) {
+    __syncthreads();
+    f32x4* red = reinterpret_cast<f32x4*>(smem);  // [WK][MT][64]
+#pragma unroll
+    for (int j = 0; j < MT; ++j) red[(wk * MT + j) * 64 + lane] = acc[j];
+    __syncthreads();
+    for (int j = wk; j < MT; j += WK) {
+      f32x4 s = red[j * 64 + lane];
+      for (int w = 1; w < WK; ++w) s += red[(w * MT + j) * 64 + lane];
+      store_out4<OUT_DT>(a, m0 + 16 * j + rsub, n0 + 4 * c0, s);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < MT; ++j) store_out4<OUT_DT>(a, m0 + 16 * j + rsub, n0 + 4 * c0, acc[j]);
+  }
+}
+
 // ---- prefill kernel --------------------------------------------------------------
 // grid (tiles, K splits); waves arranged WN (along N) x WM (along M).
 
@@ -412,10 +611,6 @@ __device__ __forceinline__ void tile_of(int id, int tiles_n, int tiles_m, int* t
   *tm = first_m + in_grp % gm;
   *tn = in_grp / gm;
 }
-
-// s_waitcnt immediate (gfx9 encoding): at most n vector memory operations of
-// this wave outstanding and every LDS/scalar access completed.
-__device__ constexpr int vmcnt_lgkm0_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4); }
 
 // Workgroup barrier for the LDS pipeline: wait until this wave's stage loads
 // (all but the newest n vector memory operations) have landed in LDS and its
@@ -680,41 +875,9 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_prefill_kernel(GemmArgs a) 
 // just-consumed stage buffer in passes of RP rows, which the storing waves
 // read into registers and store without waiting for the stores.
 //
-// The loads are inline assembly (see asm_buffer_to_lds16) and the loading
+// The loads are inline assembly (asm_buffer_to_lds16) and the loading
 // waves spread a stage's loads over the weight slices of the group being
 // multiplied, so issuing them does not hold back that wave's MFMAs.
-
-// Direct-to-LDS loads as inline assembly, for a kernel whose every wait on
-// them is an explicit stage barrier: the compiler's wait analysis does not see
-// these loads, so it never puts its own vmcnt waits in front of LDS reads or
-// barriers on their account (it does wherever its LDS alias information is
-// incomplete, and on a wave with global stores in flight such a wait would
-// stall on the stores).  M0 carries the wave's LDS destination.  The compiler
-// does not resolve hazards for inline assembly, so each load starts with five
-// wait states: enough for an SGPR operand (buffer resource or offset) written
-// by a VALU instruction such as v_readfirstlane, and for the M0 write ahead of
-// an LDS DMA.
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-__device__ __forceinline__ void asm_buffer_to_lds16(const u32x4& rsrc, uint32_t lds, int voffset,
-                                                    int soffset) {
-  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
-               :
-               : "v"(voffset), "s"(rsrc), "s"(soffset), "{m0}"(lds)
-               : "memory");
-}
-__device__ __forceinline__ void asm_global_to_lds4(const void* p, uint32_t lds) {
-  asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, off" : : "v"(p), "{m0}"(lds) : "memory");
-}
-// Raw buffer resource words (the fields make_rsrc sets) in SGPRs, for the
-// inline-assembly loads.
-__device__ __forceinline__ u32x4 rsrc_words(const void* base, uint32_t bytes) {
-  const uint64_t b = (uint64_t)(uintptr_t)base;
-  return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b),
-               (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32)),
-               (uint32_t)__builtin_amdgcn_readfirstlane((int)bytes), 0x00020000u};
-}
 
 // Largest bm / 2^i that fits in `fit` rows (the C tile leaves in equal passes).
 __host__ __device__ constexpr int pass_rows(int bm, int fit) {
@@ -982,7 +1145,7 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_persist_kernel(GemmArgs a) 
 using KernelFn = void (*)(GemmArgs);
 
 struct CfgEntry {
-  int kind;  // 1 = decode, 2 = prefill, 3 = persistent prefill
+  int kind;  // 1 = decode, 2 = prefill, 3 = persistent prefill, 4 = wide decode
   int bn, bm, waves;
   const char* name;
   KernelFn fn[3];  // [out_dt index]
@@ -1002,6 +1165,11 @@ struct CfgEntry {
     gemm_prefill_kernel<BN, BM, WN, WM, ST, kFp16>,                                            \
     gemm_prefill_kernel<BN, BM, WN, WM, ST, kBf16>}}
 
+#define DECODE_WIDE_CFG(MT, WK, UW, UA, NAME)                                                  \
+  {4, 16, 16 * MT, WK, NAME,                                                                   \
+   {gemm_decode_wide_kernel<MT, WK, UW, UA, kFp32>,                                            \
+    gemm_decode_wide_kernel<MT, WK, UW, UA, kFp16>,                                            \
+    gemm_decode_wide_kernel<MT, WK, UW, UA, kBf16>}}
 #define PERSIST_CFG(BN, BM, WN, WM, NAME)                                                      \
   {3, BN, BM, WN * WM, NAME,                                                                   \
    {gemm_persist_kernel<BN, BM, WN, WM, kFp32>, gemm_persist_kernel<BN, BM, WN, WM, kFp16>,     \
@@ -1030,6 +1198,12 @@ const CfgEntry kCfgs[] = {
     PERSIST_CFG(256, 256, 2, 4, "per_n256_m256_w8"),
     PERSIST_CFG(256, 128, 4, 2, "per_n256_m128_w8"),
     PERSIST_CFG(128, 128, 2, 2, "per_n128_m128_w4"),
+    DECODE_WIDE_CFG(4, 4, 6, 2, "dw_m64_k4"),
+    DECODE_WIDE_CFG(4, 2, 8, 2, "dw_m64_k2"),
+    DECODE_WIDE_CFG(2, 4, 6, 3, "dw_m32_k4"),
+    DECODE_WIDE_CFG(2, 2, 8, 3, "dw_m32_k2"),
+    DECODE_WIDE_CFG(1, 8, 6, 3, "dw_m16_k8"),
+    DECODE_WIDE_CFG(1, 4, 8, 3, "dw_m16_k4"),
 };
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
@@ -1169,6 +1343,14 @@ extern "C" int inferop_hip_gemm_w8a8_block(void* c, const uint8_t* a_q, const fl
     }
     hipLaunchKernelGGL(cf.fn[di], dim3((unsigned)tn, (unsigned)split, (unsigned)tm),
                        dim3(64 * cf.waves), 0, st, args);
+  } else if (cf.kind == 4) {
+    // one workgroup per 16-row weight stripe and 16*MT activation rows, the
+    // whole K range (split_k is ignored); stripe and tile rows are addressed
+    // with 32-bit offsets
+    if ((int64_t)cf.bm * k > 0x7FFFFFFF) return hipErrorInvalidValue;
+    if (tn > 0x7FFFFFFF || tm > 65535) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL(cf.fn[di], dim3((unsigned)tn, (unsigned)tm), dim3(64 * cf.waves), 0, st,
+                       args);
   } else if (cf.kind == 3) {
     // persistent: whole tiles (split_k is ignored), an even number of scale
     // groups, one workgroup per CU (two for 128x128 tiles, whose LDS allows it)

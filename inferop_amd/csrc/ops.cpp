@@ -85,6 +85,12 @@ enum GemmCfg : int32_t {
   kPerN256M256 = 19,
   kPerN256M128 = 20,
   kPerN128M128 = 21,
+  kDwM64K4 = 22,
+  kDwM64K2 = 23,
+  kDwM32K4 = 24,
+  kDwM32K2 = 25,
+  kDwM16K8 = 26,
+  kDwM16K4 = 27,
 };
 
 struct GemmChoice {
@@ -106,16 +112,24 @@ GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
     if (split > kg / 4) split = kg / 4;
     return split < 1 ? int64_t(1) : split;
   };
-  if (m > 32 && m <= 64 && !huge_k) {
-    // HBM-bound, but the activation tile is too tall to re-read from L2 per
-    // 16 weight rows: 128 weight rows x 32 activation rows per workgroup with
-    // A and B staged through LDS; the two M tiles of one N tile run back to
-    // back on one XCD and share B in its L2.  One workgroup fits a CU, so K
-    // is split up to one workgroup per CU.
-    const int64_t tiles = ((n + 127) / 128) * ((m + 31) / 32);
+  const int64_t stripes = (n + 15) / 16;  // 16-row weight stripes
+  if (m > 16 && m <= 64 && !huge_k) {
+    // HBM-bound: one workgroup per weight stripe over the whole K range with
+    // the activation tiles of all M rows; the activations, which every stripe
+    // reads again from L2, are what limits it.  Two workgroups per CU when
+    // there are more stripes than CUs.
+    const bool two = stripes > cus;
+    if (m <= 32) return {two ? kDwM32K2 : kDwM32K4, 1};
+    const int64_t per_cu = two ? 2 : 1;
+    const int64_t rounds = (stripes + cus * per_cu - 1) / (cus * per_cu);
+    const int64_t act_bytes_per_cu = rounds * per_cu * 64 * k;
+    if (act_bytes_per_cu <= 300 * 1024) return {two ? kDwM64K2 : kDwM64K4, 1};
+    // Beyond that, 64x64 tiles (the activation rows of a tile are read once
+    // per 64 weight rows) with K split up to one workgroup per CU.
+    const int64_t tiles = ((n + 63) / 64) * ((m + 63) / 64);
     int64_t split = cus / tiles;
     if (split > kg / 4) split = kg / 4;
-    return {kPreN128M32S4, int32_t(split < 1 ? 1 : split)};
+    return {kPreN64M64S4, int32_t(split < 1 ? 1 : split)};
   }
   if (m > 64 && m <= 128 && !huge_k && ((n + 127) / 128) * ((m + 127) / 128) < cus) {
     // Still HBM-bound and too few 128x128 tiles to occupy every CU: 64x64
@@ -123,15 +137,16 @@ GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
     const int64_t tiles = ((n + 63) / 64) * ((m + 63) / 64);
     return {kPreN64M64S4, int32_t(small_tile_split(tiles))};
   }
-  if (m <= 32 && !huge_k) {
+  if (m <= 16 && !huge_k) {
     // HBM-bound: a workgroup owns 16 weight rows and streams them, with the
     // 16 activation rows, through per-wave LDS slots; its waves split K.
     // Short K keeps a stripe in four waves, longer K in eight; K is split
-    // across workgroups only when the stripes alone leave CUs idle.
-    // (17 <= M <= 32 runs two M tiles over the same weight stripe, in two
-    // waves per stripe, which leaves room for twice the workgroups.)
-    const int64_t stripes = (n + 15) / 16;
-    const int32_t cfg = m > 16 ? kDecLdsK2 : kg <= 16 ? kDecLdsK4 : kDecLdsK8;
+    // across workgroups only when the stripes alone leave CUs idle.  With too
+    // few stripes to occupy three quarters of the CUs (and more than one
+    // activation row), the deeper per-wave weight rings of the wide decode
+    // kernel do better.
+    if (m > 1 && 4 * stripes < 3 * cus) return {kDwM16K4, 1};
+    const int32_t cfg = kg <= 16 ? kDecLdsK4 : kDecLdsK8;
     int64_t split = stripes < cus ? cus / stripes : 1;
     if (split > kg / 32) split = kg / 32;
     if (split < 1) split = 1;
