@@ -57,7 +57,9 @@ typedef struct {
   int32_t bm;     /* block tile along M */
   int32_t waves;  /* waves per workgroup */
   int32_t kind;   /* 1 = decode (16-row weight stripes), 2 = LDS-staged output tiles,
-                     3 = persistent LDS-staged tiles (split_k ignored, K/128 even) */
+                     3 = persistent LDS-staged tiles (split_k ignored, K/128 even),
+                     4 = wide decode: a weight stripe over all of K with bm activation
+                         rows (split_k ignored) */
   const char* name;
 } inferop_gemm_cfg_info;
 
