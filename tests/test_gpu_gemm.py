@@ -180,6 +180,28 @@ def test_persistent_kernels_match_tiled_kernel(name):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("name", ["dw_m64_k4", "dw_m64_k2", "dw_m32_k4", "dw_m32_k2",
+                                  "dw_m16_k8", "dw_m16_k4"])
+def test_wide_decode_kernels(name):
+    # one workgroup per 16-row weight stripe over all of K: ragged stripes,
+    # several activation tiles (M past one tile), waves left without groups
+    # (K/128 below the wave count), odd group counts, every output dtype
+    device()
+    cfg = _cfg(name)
+    cases = [(1, 2112, 7168), (5, 300, 256), (17, 4096, 2048), (48, 1000, 1152), (64, 2112, 7168),
+             (70, 520, 384)]
+    for (m, n, k) in cases:
+        print(f"{name} {m}x{n}x{k}", flush=True)
+        _, aq, as_, bq, bs = _host_case(m, n, k, seed=m + n)
+        want = oracle.gemm(aq, as_, bq, bs)
+        args = [to_dev(v) for v in (aq, as_, bq, bs)]
+        for out in ("bf16", "fp16", "fp32"):
+            c = _gemm(*args, m, n, k, out, cfg, 1)
+            assert_gemm_close(out_to_f32(c), want, f"{name} {m}x{n}x{k} {out}")
+            assert torch.equal(_gemm(*args, m, n, k, out, cfg, 1), c)  # no atomics: repeatable
+
+
+@pytest.mark.gpu
 def test_output_dtypes_and_odd_n():
     device()
     for (m, n, k) in [(40, 130, 256), (5, 7, 128), (129, 1, 384)]:
