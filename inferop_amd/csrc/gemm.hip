@@ -103,6 +103,15 @@ __device__ __forceinline__ void asm_buffer_to_lds16(const u32x4& rsrc, uint32_t 
                : "v"(voffset), "s"(rsrc), "s"(soffset), "{m0}"(lds)
                : "memory");
 }
+// Same with the non-temporal hint: for data read exactly once (streamed
+// weights), so it does not push data that is read again out of the L2.
+__device__ __forceinline__ void asm_buffer_to_lds16_nt(const u32x4& rsrc, uint32_t lds,
+                                                       int voffset, int soffset) {
+  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen nt lds"
+               :
+               : "v"(voffset), "s"(rsrc), "s"(soffset), "{m0}"(lds)
+               : "memory");
+}
 __device__ __forceinline__ void asm_global_to_lds4(const void* p, uint32_t lds) {
   asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, off" : : "v"(p), "{m0}"(lds) : "memory");
 }
@@ -474,25 +483,37 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_lds_kernel(GemmArgs a) {
 // A workgroup owns one 16-row weight stripe over the whole K range and MT
 // 16-row activation tiles; its WK waves split the scale groups and are summed
 // through LDS at the end (no split-K, so no round trip through device-coherent
-// partials).  Each weight byte leaves HBM once; the activations, shared by
-// every stripe, come from L2.  A wave streams its groups through two private
-// rings: UW weight slots (2 KB each), refilled UW groups ahead, so enough HBM
-// bytes are in flight to cover the latency, and UA activation slots (MT tiles,
-// their scales and the weight scale), refilled UA groups ahead from L2.
-// The loads are inline assembly issued in a fixed pattern, so a single
-// constant vmcnt wait covers the next group in every iteration (tail loads
-// re-read the last group into the slot just consumed).
-template <int MT, int WK, int UW, int UA, int OUT_DT>
+// partials).  Each weight byte leaves HBM once (non-temporal loads, so the
+// stream does not evict the activations); the activations, shared by every
+// stripe, come from L2.  A wave streams its groups through two private rings:
+// UW weight slots (2 KB each), refilled UW groups ahead, and UA activation
+// slots (MT tiles), refilled UA groups ahead.  The loads are inline assembly
+// issued in a fixed pattern, so a single constant vmcnt wait covers the next
+// group in every iteration; past the wave's last group the pattern continues
+// with 4-byte loads of a weight scale (kept only for the count).
+//
+// Scales: with PRE, a wave loads the activation scales of its MT tiles and the
+// weight scales for all its groups into LDS once, before the rings start, as
+// row-contiguous runs (a per-group load of 16*MT activation scales touches
+// 16*MT cache lines, more than the weight slice itself).  That needs at most
+// wide_scale_cap(MT) groups per wave; longer ranges use the kernel without
+// PRE, whose activation slots also carry that group's scales.
+__host__ __device__ constexpr int wide_scale_cap(int mt) { return mt == 1 ? 32 : 16; }
+
+template <int MT, int WK, int UW, int UA, bool PRE, int OUT_DT>
 __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
-  constexpr int kW = 2048;                          // 16 weight rows x 128 B
-  constexpr int kOffSa = MT * 2048;                 // in an activation slot
+  constexpr int kW = 2048;                            // 16 weight rows x 128 B
+  constexpr int kCap = wide_scale_cap(MT);
+  constexpr int kOffSa = MT * 2048;                   // in an activation slot (no PRE)
   constexpr int kOffSb = kOffSa + 256;
-  constexpr int kA = MT * 2048 + 512;               // MT tiles + 64 sa + 64 sb
-  constexpr int kWave = UW * kW + UA * kA;
-  constexpr int kPerIter = 2 + 2 * MT + 2;          // loads issued per group
-  constexpr int kWait = (UA - 1) * kPerIter;        // loads that may stay in flight
+  constexpr int kA = MT * 2048 + (PRE ? 0 : 512);     // MT tiles (+ 64 sa + 64 sb)
+  constexpr int kSaF = PRE ? 16 * MT * kCap : 0;      // preloaded sa floats, [row][group]
+  constexpr int kScale = PRE ? kSaF * 4 + 256 : 0;    // + up to 64 sb floats
+  constexpr int kWave = UW * kW + UA * kA + kScale;
+  constexpr int kPerIter = 2 + 2 * MT + (PRE ? 0 : 2);  // loads issued per group
+  constexpr int kWait = (UA - 1) * kPerIter;          // loads that may stay in flight
   static_assert(UW >= UA && UA >= 2 && kWait <= 63, "ring sizes");
-  static_assert(MT >= 1 && MT <= 4, "1 to 4 activation tiles");
+  static_assert(MT >= 1 && MT <= 4 && kCap <= 64, "1 to 4 activation tiles");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[WK * kWave];
 
   const int lane = threadIdx.x & 63;
@@ -510,6 +531,9 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
   uint8_t* const wave_lds = smem + wk * kWave;
   const uint32_t wbase = lds_addr(wave_lds);
   const uint32_t abase = wbase + UW * kW;
+  const uint32_t sbase = abase + UA * kA;
+  const float* const sa_l = reinterpret_cast<const float*>(wave_lds + UW * kW + UA * kA);
+  const float* const sb_l = sa_l + kSaF;
 
   f32x4 acc[MT];
 #pragma unroll
@@ -519,26 +543,50 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
     // rows past the end of A or B read as zeros
     const u32x4 rB = rsrc_words(a.bq + (int64_t)n0 * K, (uint32_t)(min(16, N - n0) * K));
     const u32x4 rA = rsrc_words(a.aq + (int64_t)m0 * K, (uint32_t)(min(16 * MT, M - m0) * K));
-    const float* sa_src = a.as + (int64_t)(m0 + min(lane % (16 * MT), M - 1 - m0)) * KG;
-    const float* sb_src = a.bs + (int64_t)min(n0 >> 7, NB - 1) * KG;
+    const float* sb_src = a.bs + (int64_t)min(n0 >> 7, NB - 1) * KG + gw0;
+    const float* sa_src = a.as + (int64_t)(m0 + min(lane % (16 * MT), M - 1 - m0)) * KG + gw0;
+    if constexpr (PRE) {
+      // entry (r, g) at float r * cnt + g: consecutive lanes read consecutive
+      // groups of one activation row
+      const int E = 16 * MT * cnt;
+      for (int t = 0; t * 64 < E; ++t) {
+        const int idx = min(t * 64 + lane, E - 1);
+        const int r = idx / cnt, g = idx - r * cnt;
+        asm_global_to_lds4(a.as + (int64_t)min(m0 + r, M - 1) * KG + gw0 + g, sbase + t * 256);
+      }
+      asm_global_to_lds4(sb_src + min(lane, cnt - 1), sbase + kSaF * 4);
+    }
     auto issue_w = [&](int i) {  // group gw0 + i into weight slot i % UW
-      const int g = gw0 + min(i, cnt - 1);
       const uint32_t dst = wbase + (uint32_t)(i % UW) * kW;
-      asm_buffer_to_lds16(rB, dst, loff, g * 128);
-      asm_buffer_to_lds16(rB, dst + 1024, loff, 8 * K + g * 128);
+      if (i >= cnt) {
+        asm_global_to_lds4(sb_src, dst);
+        asm_global_to_lds4(sb_src, dst);
+        return;
+      }
+      const int g = gw0 + i;
+      asm_buffer_to_lds16_nt(rB, dst, loff, g * 128);
+      asm_buffer_to_lds16_nt(rB, dst + 1024, loff, 8 * K + g * 128);
     };
     auto issue_a = [&](int i) {  // group gw0 + i into activation slot i % UA
-      const int g = gw0 + min(i, cnt - 1);
       const uint32_t dst = abase + (uint32_t)(i % UA) * kA;
+      if (i >= cnt) {
 #pragma unroll
-      for (int h = 0; h < 2 * MT; ++h) asm_buffer_to_lds16(rA, dst + h * 1024, loff, 8 * h * K + g * 128);
-      asm_global_to_lds4(sa_src + g, dst + kOffSa);
-      asm_global_to_lds4(sb_src + g, dst + kOffSb);
+        for (int h = 0; h < kPerIter - 2; ++h) asm_global_to_lds4(sb_src, dst);
+        return;
+      }
+      const int g = gw0 + i;
+#pragma unroll
+      for (int h = 0; h < 2 * MT; ++h)
+        asm_buffer_to_lds16(rA, dst + h * 1024, loff, 8 * h * K + g * 128);
+      if constexpr (!PRE) {
+        asm_global_to_lds4(sa_src + i, dst + kOffSa);
+        asm_global_to_lds4(sb_src + i, dst + kOffSb);
+      }
     };
     // Prologue in the loop's issue pattern: the weight slots beyond the
     // activation depth first, then (weight, activation) pairs; after it, and
     // after every iteration, exactly kWait loads follow the activations of the
-    // group consumed next.
+    // group consumed next (the scale preload comes before all of them).
     for (int s = 0; s < UW - UA; ++s) issue_w(s);
 #pragma unroll
     for (int j = 0; j < UA; ++j) {
@@ -552,11 +600,13 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
       const uint8_t* W = wave_lds + (i % UW) * kW;
       const uint8_t* A = wave_lds + UW * kW + (i % UA) * kA;
       const i32x8 wop = lds_operand(W, rsub, c0);
-      const float sb = reinterpret_cast<const float*>(A + kOffSb)[0];
+      const float sb = PRE ? sb_l[i] : reinterpret_cast<const float*>(A + kOffSb)[0];
 #pragma unroll
       for (int j = 0; j < MT; ++j) {
         const f32x4 pv = mfma_group(wop, lds_operand(A + j * 2048, rsub, c0));
-        const float sc = reinterpret_cast<const float*>(A + kOffSa)[16 * j + rsub] * sb;
+        const float sa = PRE ? sa_l[(16 * j + rsub) * cnt + i]
+                             : reinterpret_cast<const float*>(A + kOffSa)[16 * j + rsub];
+        const float sc = sa * sb;
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[j][r] = __builtin_fmaf(pv[r], sc, acc[j][r]);
       }
@@ -1149,6 +1199,9 @@ struct CfgEntry {
   int bn, bm, waves;
   const char* name;
   KernelFn fn[3];  // [out_dt index]
+  // wide decode only: the same configuration without the scale preload, for
+  // more than wide_scale_cap(MT) groups per wave
+  KernelFn fn_long[3];
 };
 
 #define DECODE_CFG(MT, WK, U, NAME)                                                           \
@@ -1166,10 +1219,17 @@ struct CfgEntry {
     gemm_prefill_kernel<BN, BM, WN, WM, ST, kBf16>}}
 
 #define DECODE_WIDE_CFG(MT, WK, UW, UA, NAME)                                                  \
-  {4, 16, 16 * MT, WK, NAME,                                                                   \
-   {gemm_decode_wide_kernel<MT, WK, UW, UA, kFp32>,                                            \
-    gemm_decode_wide_kernel<MT, WK, UW, UA, kFp16>,                                            \
-    gemm_decode_wide_kernel<MT, WK, UW, UA, kBf16>}}
+  {4,                                                                                          \
+   16,                                                                                         \
+   16 * MT,                                                                                    \
+   WK,                                                                                         \
+   NAME,                                                                                       \
+   {gemm_decode_wide_kernel<MT, WK, UW, UA, true, kFp32>,                                      \
+    gemm_decode_wide_kernel<MT, WK, UW, UA, true, kFp16>,                                      \
+    gemm_decode_wide_kernel<MT, WK, UW, UA, true, kBf16>},                                     \
+   {gemm_decode_wide_kernel<MT, WK, UW, UA, false, kFp32>,                                     \
+    gemm_decode_wide_kernel<MT, WK, UW, UA, false, kFp16>,                                     \
+    gemm_decode_wide_kernel<MT, WK, UW, UA, false, kBf16>}}
 #define PERSIST_CFG(BN, BM, WN, WM, NAME)                                                      \
   {3, BN, BM, WN * WM, NAME,                                                                   \
    {gemm_persist_kernel<BN, BM, WN, WM, kFp32>, gemm_persist_kernel<BN, BM, WN, WM, kFp16>,     \
@@ -1198,12 +1258,13 @@ const CfgEntry kCfgs[] = {
     PERSIST_CFG(256, 256, 2, 4, "per_n256_m256_w8"),
     PERSIST_CFG(256, 128, 4, 2, "per_n256_m128_w8"),
     PERSIST_CFG(128, 128, 2, 2, "per_n128_m128_w4"),
-    DECODE_WIDE_CFG(4, 4, 6, 2, "dw_m64_k4"),
-    DECODE_WIDE_CFG(4, 2, 8, 2, "dw_m64_k2"),
-    DECODE_WIDE_CFG(2, 4, 6, 3, "dw_m32_k4"),
-    DECODE_WIDE_CFG(2, 2, 8, 3, "dw_m32_k2"),
-    DECODE_WIDE_CFG(1, 8, 6, 3, "dw_m16_k8"),
-    DECODE_WIDE_CFG(1, 4, 8, 3, "dw_m16_k4"),
+    DECODE_WIDE_CFG(4, 4, 2, 2, "dw_m64_k4_w2a2"),
+    DECODE_WIDE_CFG(4, 2, 8, 2, "dw_m64_k2_w8a2"),
+    DECODE_WIDE_CFG(2, 4, 4, 4, "dw_m32_k4_w4a4"),
+    DECODE_WIDE_CFG(2, 2, 6, 6, "dw_m32_k2_w6a6"),
+    DECODE_WIDE_CFG(1, 8, 3, 3, "dw_m16_k8_w3a3"),
+    DECODE_WIDE_CFG(1, 4, 6, 6, "dw_m16_k4_w6a6"),
+    DECODE_WIDE_CFG(4, 4, 6, 2, "dw_m64_k4_w6a2"),
 };
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
@@ -1346,11 +1407,13 @@ extern "C" int inferop_hip_gemm_w8a8_block(void* c, const uint8_t* a_q, const fl
   } else if (cf.kind == 4) {
     // one workgroup per 16-row weight stripe and 16*MT activation rows, the
     // whole K range (split_k is ignored); stripe and tile rows are addressed
-    // with 32-bit offsets
+    // with 32-bit offsets.  The scale preload holds wide_scale_cap(MT) groups
+    // per wave; a longer range per wave takes the kernel without it.
     if ((int64_t)cf.bm * k > 0x7FFFFFFF) return hipErrorInvalidValue;
     if (tn > 0x7FFFFFFF || tm > 65535) return hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL(cf.fn[di], dim3((unsigned)tn, (unsigned)tm), dim3(64 * cf.waves), 0, st,
-                       args);
+    const int64_t per_wave = (kg + cf.waves - 1) / cf.waves;
+    const KernelFn fn = per_wave <= wide_scale_cap(cf.bm / 16) ? cf.fn[di] : cf.fn_long[di];
+    hipLaunchKernelGGL(fn, dim3((unsigned)tn, (unsigned)tm), dim3(64 * cf.waves), 0, st, args);
   } else if (cf.kind == 3) {
     // persistent: whole tiles (split_k is ignored), an even number of scale
     // groups, one workgroup per CU (two for 128x128 tiles, whose LDS allows it)

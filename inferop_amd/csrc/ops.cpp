@@ -91,6 +91,7 @@ enum GemmCfg : int32_t {
   kDwM32K2 = 25,
   kDwM16K8 = 26,
   kDwM16K4 = 27,
+  kDwM64K4W6 = 28,
 };
 
 struct GemmChoice {
@@ -114,22 +115,37 @@ GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
   };
   const int64_t stripes = (n + 15) / 16;  // 16-row weight stripes
   if (m > 16 && m <= 64 && !huge_k) {
-    // HBM-bound: one workgroup per weight stripe over the whole K range with
-    // the activation tiles of all M rows; the activations, which every stripe
-    // reads again from L2, are what limits it.  Two workgroups per CU when
-    // there are more stripes than CUs.
+    // HBM-bound.  The wide decode kernel gives a workgroup one weight stripe
+    // over the whole K range with the activation tiles of all M rows (no
+    // split-K); the activations, which every stripe reads again from L2, are
+    // what limits it, so it serves up to about one stripe per CU.  Two
+    // workgroups per CU when there are more stripes than CUs and each wave
+    // still preloads all its scales (at most 32 scale groups over two waves).
     const bool two = stripes > cus;
-    if (m <= 32) return {two ? kDwM32K2 : kDwM32K4, 1};
-    const int64_t per_cu = two ? 2 : 1;
-    const int64_t rounds = (stripes + cus * per_cu - 1) / (cus * per_cu);
-    const int64_t act_bytes_per_cu = rounds * per_cu * 64 * k;
-    if (act_bytes_per_cu <= 300 * 1024) return {two ? kDwM64K2 : kDwM64K4, 1};
-    // Beyond that, 64x64 tiles (the activation rows of a tile are read once
-    // per 64 weight rows) with K split up to one workgroup per CU.
-    const int64_t tiles = ((n + 63) / 64) * ((m + 63) / 64);
-    int64_t split = cus / tiles;
-    if (split > kg / 4) split = kg / 4;
-    return {kPreN64M64S4, int32_t(split < 1 ? 1 : split)};
+    if (m <= 32) return {two && kg <= 32 ? kDwM32K2 : kDwM32K4, 1};
+    if (stripes <= cus && kg >= 32) {
+      // with a quarter of the CUs or more left without a stripe, 128x32
+      // tiles with K split across all CUs do better
+      if (4 * stripes <= 3 * cus) {
+        const int64_t tiles = ((n + 127) / 128) * ((m + 31) / 32);
+        int64_t split = cus / tiles;
+        if (split > kg / 4) split = kg / 4;
+        return {kPreN128M32S4, int32_t(split < 1 ? 1 : split)};
+      }
+      return {kDwM64K4, 1};
+    }
+    if (stripes <= 2 * cus && kg >= 8 && kg <= 32) return {kDwM64K2, 1};
+    // Beyond that, 128x64 tiles (a tile's activation rows are read once per
+    // 128 weight rows); with a long K, split it so about two workgroups run
+    // per CU (at most four splits: each split adds a partial round trip).
+    const int64_t tiles = ((n + 127) / 128) * ((m + 63) / 64);
+    int64_t split = 1;
+    if (kg >= 32) {
+      split = (2 * cus + tiles - 1) / tiles;
+      if (split > 4) split = 4;
+      if (split > kg / 4) split = kg / 4;
+    }
+    return {kPreN128M64S4, int32_t(split < 1 ? 1 : split)};
   }
   if (m > 64 && m <= 128 && !huge_k && ((n + 127) / 128) * ((m + 127) / 128) < cus) {
     // Still HBM-bound and too few 128x128 tiles to occupy every CU: 64x64
@@ -138,19 +154,20 @@ GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
     return {kPreN64M64S4, int32_t(small_tile_split(tiles))};
   }
   if (m <= 16 && !huge_k) {
-    // HBM-bound: a workgroup owns 16 weight rows and streams them, with the
-    // 16 activation rows, through per-wave LDS slots; its waves split K.
-    // Short K keeps a stripe in four waves, longer K in eight; K is split
-    // across workgroups only when the stripes alone leave CUs idle.  With too
-    // few stripes to occupy three quarters of the CUs (and more than one
-    // activation row), the deeper per-wave weight rings of the wide decode
-    // kernel do better.
-    if (m > 1 && 4 * stripes < 3 * cus) return {kDwM16K4, 1};
-    const int32_t cfg = kg <= 16 ? kDecLdsK4 : kDecLdsK8;
-    int64_t split = stripes < cus ? cus / stripes : 1;
-    if (split > kg / 32) split = kg / 32;
-    if (split < 1) split = 1;
-    return {cfg, int32_t(split)};
+    // HBM-bound: a workgroup owns 16 weight rows over the whole K range.  For
+    // a short K (at most 16 scale groups) with at least one stripe per CU,
+    // the decode kernel with LDS-staged activations (four waves splitting K);
+    // otherwise the wide decode kernel with eight waves, whose three-deep
+    // rings and preloaded scales keep a stripe streaming.  A long K over
+    // stripes for fewer than half the CUs is split across workgroups on the
+    // LDS-staged kernel (at least 32 scale groups per split).
+    if (kg <= 16 && stripes >= cus) return {kDecLdsK4, 1};
+    if (2 * stripes <= cus && kg >= 64) {
+      int64_t split = cus / stripes;
+      if (split > kg / 32) split = kg / 32;
+      return {kDecLdsK8, int32_t(split)};
+    }
+    return {kDwM16K8, 1};
   }
   if (m <= 64 || huge_k) {
     // HBM-bound: a workgroup owns 16 weight rows; its WK waves split the

@@ -180,16 +180,19 @@ def test_persistent_kernels_match_tiled_kernel(name):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("name", ["dw_m64_k4", "dw_m64_k2", "dw_m32_k4", "dw_m32_k2",
-                                  "dw_m16_k8", "dw_m16_k4"])
+@pytest.mark.parametrize("name", ["dw_m64_k4_w2a2", "dw_m64_k2_w8a2", "dw_m32_k4_w4a4",
+                                  "dw_m32_k2_w6a6", "dw_m16_k8_w3a3", "dw_m16_k4_w6a6",
+                                  "dw_m64_k4_w6a2"])
 def test_wide_decode_kernels(name):
     # one workgroup per 16-row weight stripe over all of K: ragged stripes,
     # several activation tiles (M past one tile), waves left without groups
-    # (K/128 below the wave count), odd group counts, every output dtype
+    # (K/128 below the wave count), odd group counts, every output dtype; the
+    # last two shapes give some configurations more scale groups per wave than
+    # the scale preload holds (the kernel without it)
     device()
     cfg = _cfg(name)
     cases = [(1, 2112, 7168), (5, 300, 256), (17, 4096, 2048), (48, 1000, 1152), (64, 2112, 7168),
-             (70, 520, 384)]
+             (70, 520, 384), (3, 640, 18432), (40, 520, 9216)]
     for (m, n, k) in cases:
         print(f"{name} {m}x{n}x{k}", flush=True)
         _, aq, as_, bq, bs = _host_case(m, n, k, seed=m + n)

@@ -173,6 +173,21 @@ def test_gemm_selection_covers_configs():
     # a long K over too few weight stripes to occupy every CU is split
     assert inferop_amd.gemm_select(1, 512, 8 * 7168)[1] > 1
     assert inferop_amd.gemm_select(1, 4096, 7168)[1] == 1
+    # decode shapes: wide decode kernels for long K or few stripes, the
+    # LDS-staged decode kernel for short K over many stripes, 128x32 tiles
+    # with split-K when M > 32 leaves most CUs without a stripe
+    def sel(m, n, k):
+        cfg, split = inferop_amd.gemm_select(m, n, k)
+        return names[cfg], split
+    assert sel(1, 7168, 2048) == ("decl_k4_u4", 1)
+    assert sel(1, 4096, 7168) == ("dw_m16_k8_w3a3", 1)
+    assert sel(16, 2112, 7168) == ("dw_m16_k8_w3a3", 1)
+    assert sel(32, 7168, 2048) == ("dw_m32_k2_w6a6", 1)
+    assert sel(32, 4096, 7168) == ("dw_m32_k4_w4a4", 1)
+    assert sel(64, 7168, 2048) == ("dw_m64_k2_w8a2", 1)
+    assert sel(64, 4096, 7168) == ("dw_m64_k4_w2a2", 1)
+    assert sel(64, 2112, 7168) == ("pre_n128_m32_w8_s4", 7)
+    assert sel(64, 36864, 7168) == ("pre_n128_m64_w8_s4", 2)
     # 256x256 prefill tiles run on the persistent kernel when K / 128 is even,
     # on the one-tile-per-workgroup kernel otherwise
     assert names[inferop_amd.gemm_select(4096, 7168, 16384)[0]] == "per_n256_m256_w8"
