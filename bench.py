@@ -44,7 +44,7 @@ PREFILL_LAUNCHES = 20
 # WRITE_SIZE from rocprofv3 runs of `bench.py --traffic-pass`, each scaled by
 # what the counter reads for a 256 MiB streaming kernel in the same process
 # (per-launch table and commands: profiles/decode_step_hbm_traffic.md).
-DECODE_GEMM_TRAFFIC_BYTES = 22456723
+DECODE_GEMM_TRAFFIC_BYTES = 21866023
 
 
 def quant_bytes(m, k, in_bytes=2):
@@ -253,6 +253,30 @@ def main():
         torch.cuda.empty_cache()
 
         # ---------------- prefill GEMM (configs[2], M = 4096) ----------------
+        def vendor_rowwise_tflops(q, ws, m, n, k):
+            """The platform's FP8 GEMM on the same E4M3 bytes, for reference:
+            torch._scaled_mm (hipBLASLt) with one scale per row of A and of B --
+            a simpler operation than the blockwise one (no per-group
+            promotion), so an upper reference for its throughput, not a
+            competitor computing the same result.  None where unavailable."""
+            try:
+                a8 = q.view(torch.float8_e4m3fn)
+                bs8 = [bq.view(torch.float8_e4m3fn) for bq, _ in ws]
+                sa = torch.rand((m, 1), generator=gen, device=dev) + 0.5
+                sb = torch.rand((1, n), generator=gen, device=dev) + 0.5
+
+                def v(i):
+                    torch._scaled_mm(a8, bs8[i % len(bs8)].t(), scale_a=sa, scale_b=sb,
+                                     out_dtype=torch.bfloat16)
+
+                gv = capture(lambda: [v(i) for i in range(PREFILL_LAUNCHES)])
+                time_graphs([gv], 2)
+                vus = time_graphs([gv], 5) / PREFILL_LAUNCHES * 1e3
+                del gv
+                return round(2.0 * m * n * k / (vus * 1e-6) / 1e12, 1)
+            except (RuntimeError, AttributeError, TypeError):
+                return None
+
         pre = []
         m = 4096
         for (n, k) in PREFILL_NK:
@@ -276,12 +300,18 @@ def main():
             pre.append({"m": m, "n": n, "k": k, "us": round(us, 2), "tflops": round(tflops, 1),
                         "frac_of_peak": round(tflops / FP8_PEAK_TFLOPS, 4),
                         "frac_of_roofline": round(tflops / bound, 4),
-                        "kernel": ia.gemm_config_name(cfg), "split_k": split})
+                        "kernel": ia.gemm_config_name(cfg), "split_k": split,
+                        "vendor_rowwise_tflops": vendor_rowwise_tflops(q, ws, m, n, k)})
             del a, q, s, ws, c, gg
         tot_flops = sum(2.0 * p["m"] * p["n"] * p["k"] for p in pre)
         tot_s = sum(p["us"] for p in pre) * 1e-6
+        vend = [p["vendor_rowwise_tflops"] for p in pre]
+        vend_tflops = (round(tot_flops / sum(2.0 * p["m"] * p["n"] * p["k"] / (t * 1e12)
+                                             for p, t in zip(pre, vend)) / 1e12, 1)
+                       if all(vend) else None)
         result["prefill"] = {
             "tflops": round(tot_flops / tot_s / 1e12, 1),
+            "vendor_rowwise_tflops": vend_tflops,
             "frac_of_peak": round(tot_flops / tot_s / 1e12 / FP8_PEAK_TFLOPS, 4),
             "peak_tflops": FP8_PEAK_TFLOPS, "shapes": pre,
             "roofline": {"bound": "mfma", "kernel": "w8a8 block-FP8 GEMM, prefill tiles",
