@@ -497,8 +497,10 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_lds_kernel(GemmArgs a) {
 // row-contiguous runs (a per-group load of 16*MT activation scales touches
 // 16*MT cache lines, more than the weight slice itself).  That needs at most
 // wide_scale_cap(MT) groups per wave; longer ranges use the kernel without
-// PRE, whose activation slots also carry that group's scales.
-__host__ __device__ constexpr int wide_scale_cap(int mt) { return mt == 1 ? 32 : 16; }
+// PRE, whose activation slots also carry that group's scales.  The cap keeps
+// the configurations small enough for two workgroups per CU (LDS), which is
+// worth more than preloading for longer K.
+__host__ __device__ constexpr int wide_scale_cap(int) { return 16; }
 
 template <int MT, int WK, int UW, int UA, bool PRE, int OUT_DT>
 __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
@@ -1259,12 +1261,12 @@ const CfgEntry kCfgs[] = {
     PERSIST_CFG(256, 128, 4, 2, "per_n256_m128_w8"),
     PERSIST_CFG(128, 128, 2, 2, "per_n128_m128_w4"),
     DECODE_WIDE_CFG(4, 4, 2, 2, "dw_m64_k4_w2a2"),
-    DECODE_WIDE_CFG(4, 2, 8, 2, "dw_m64_k2_w8a2"),
-    DECODE_WIDE_CFG(2, 4, 4, 4, "dw_m32_k4_w4a4"),
-    DECODE_WIDE_CFG(2, 2, 6, 6, "dw_m32_k2_w6a6"),
+    DECODE_WIDE_CFG(4, 2, 4, 2, "dw_m64_k2_w4a2"),
+    DECODE_WIDE_CFG(2, 4, 2, 2, "dw_m32_k4_w2a2"),
+    DECODE_WIDE_CFG(1, 2, 8, 8, "dw_m16_k2_w8a8"),
     DECODE_WIDE_CFG(1, 8, 3, 3, "dw_m16_k8_w3a3"),
-    DECODE_WIDE_CFG(1, 4, 6, 6, "dw_m16_k4_w6a6"),
-    DECODE_WIDE_CFG(4, 4, 6, 2, "dw_m64_k4_w6a2"),
+    DECODE_WIDE_CFG(1, 4, 3, 3, "dw_m16_k4_w3a3"),
+    DECODE_WIDE_CFG(1, 8, 2, 2, "dw_m16_k8_w2a2"),
 };
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 

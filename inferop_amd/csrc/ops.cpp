@@ -88,10 +88,10 @@ enum GemmCfg : int32_t {
   kDwM64K4 = 22,
   kDwM64K2 = 23,
   kDwM32K4 = 24,
-  kDwM32K2 = 25,
+  kDwM16K2 = 25,
   kDwM16K8 = 26,
   kDwM16K4 = 27,
-  kDwM64K4W6 = 28,
+  kDwM16K8W2 = 28,
 };
 
 struct GemmChoice {
@@ -118,11 +118,9 @@ GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
     // HBM-bound.  The wide decode kernel gives a workgroup one weight stripe
     // over the whole K range with the activation tiles of all M rows (no
     // split-K); the activations, which every stripe reads again from L2, are
-    // what limits it, so it serves up to about one stripe per CU.  Two
-    // workgroups per CU when there are more stripes than CUs and each wave
-    // still preloads all its scales (at most 32 scale groups over two waves).
-    const bool two = stripes > cus;
-    if (m <= 32) return {two && kg <= 32 ? kDwM32K2 : kDwM32K4, 1};
+    // what limits it, so it serves up to about one stripe per CU for a long K
+    // and two for K <= 4096 (the configurations fit two workgroups per CU).
+    if (m <= 32) return {kDwM32K4, 1};
     if (stripes <= cus && kg >= 32) {
       // with a quarter of the CUs or more left without a stripe, 128x32
       // tiles with K split across all CUs do better
@@ -154,20 +152,23 @@ GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
     return {kPreN64M64S4, int32_t(small_tile_split(tiles))};
   }
   if (m <= 16 && !huge_k) {
-    // HBM-bound: a workgroup owns 16 weight rows over the whole K range.  For
-    // a short K (at most 16 scale groups) with at least one stripe per CU,
-    // the decode kernel with LDS-staged activations (four waves splitting K);
-    // otherwise the wide decode kernel with eight waves, whose three-deep
-    // rings and preloaded scales keep a stripe streaming.  A long K over
-    // stripes for fewer than half the CUs is split across workgroups on the
-    // LDS-staged kernel (at least 32 scale groups per split).
-    if (kg <= 16 && stripes >= cus) return {kDecLdsK4, 1};
+    // HBM-bound: a workgroup owns 16 weight rows over the whole K range on
+    // the wide decode kernel.  A long K over stripes for fewer than half the
+    // CUs is split across workgroups on the LDS-staged decode kernel (at
+    // least 32 scale groups per split).  Otherwise: K beyond 8192 on two
+    // waves with eight-deep rings; a stripe per CU or fewer on eight waves
+    // with three-deep rings (all CUs busy with one workgroup each); many
+    // stripes on the configurations that fit two workgroups per CU (four
+    // waves three deep, or eight waves two deep beyond two stripes per CU).
     if (2 * stripes <= cus && kg >= 64) {
       int64_t split = cus / stripes;
       if (split > kg / 32) split = kg / 32;
       return {kDecLdsK8, int32_t(split)};
     }
-    return {kDwM16K8, 1};
+    if (kg > 64) return {kDwM16K2, 1};
+    if (kg <= 16) return {kDwM16K4, 1};
+    if (stripes <= cus) return {kDwM16K8, 1};
+    return {stripes > 2 * cus ? kDwM16K8W2 : kDwM16K4, 1};
   }
   if (m <= 64 || huge_k) {
     // HBM-bound: a workgroup owns 16 weight rows; its WK waves split the
