@@ -88,6 +88,21 @@ int inferop_fused_add_rmsnorm_quant_fp8(void* residual, void* q, void* scales, c
                                         const void* weight, int32_t dt, int64_t rows, int64_t cols,
                                         float eps, int32_t group_size, void* stream);
 
+/* --- extension: grouped blockwise-FP8 GEMM over MoE experts (no counterpart
+ * in the reference's ops.h; its roadmap lists it, docs/ROADMAP.md:39) ---
+ * Contiguous layout, as inferop::w8a8_block_fp8_grouped_gemm in ops.h:
+ * a_q [m, k] rows sorted by expert, expert e owning rows
+ * [expert_offsets[e], expert_offsets[e+1]) (device int32, num_experts + 1
+ * entries, clamped to [0, m] on the device); b_q [num_experts, n, k];
+ * b_scales [num_experts, ceil(n/128), k/128]; c [m, n].  The GEMM's shape
+ * rules (INFEROP_ERR_SHAPE with its diagnostic) plus num_experts >= 1 and
+ * m >= 0; m = 0 returns INFEROP_OK without a launch. */
+int inferop_w8a8_block_fp8_grouped_gemm(void* c, const void* a_q, const void* a_scales,
+                                        const void* b_q, const void* b_scales,
+                                        const int32_t* expert_offsets, int64_t m, int64_t n,
+                                        int64_t k, int64_t num_experts, int32_t group_size,
+                                        int32_t block_n, int32_t out_dt, void* stream);
+
 /* --- tuning and testing (no counterpart in the reference) ---
  * The GEMM with an explicit kernel configuration and split-K factor instead
  * of the automatic gfx950 choice.  config in [0, inferop_gemm_num_configs()).
@@ -101,6 +116,16 @@ int inferop_w8a8_block_fp8_gemm_config(void* c, const void* a_q, const void* a_s
                                        int32_t split_k, void* stream);
 /* The configuration and split-K factor the automatic choice would use. */
 int inferop_gemm_select(int64_t m, int64_t n, int64_t k, int32_t* config, int32_t* split_k);
+/* The grouped GEMM with an explicit configuration: one of the tiled
+ * configurations with a grouped variant (others return INFEROP_ERR_ARGUMENT);
+ * and the configuration the automatic choice would use. */
+int inferop_w8a8_block_fp8_grouped_gemm_config(void* c, const void* a_q, const void* a_scales,
+                                               const void* b_q, const void* b_scales,
+                                               const int32_t* expert_offsets, int64_t m,
+                                               int64_t n, int64_t k, int64_t num_experts,
+                                               int32_t out_dt, int32_t config, void* stream);
+int inferop_grouped_gemm_select(int64_t m, int64_t n, int64_t k, int64_t num_experts,
+                                int32_t* config);
 
 /* --- diagnostics (no counterpart in the reference) ---
  * Compares, on the current device, the hardware E4M3 conversions the fast

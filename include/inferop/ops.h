@@ -108,4 +108,21 @@ void fused_add_rmsnorm_quant_fp8(void* residual, void* q, void* scales, const vo
                                  float eps = 1e-6f, int group_size = 128,
                                  void* stream = nullptr);
 
+// --- extension: grouped W8A8 blockwise-FP8 GEMM over MoE experts --------------
+// No counterpart in the reference ops.h: its roadmap lists the grouped GEMM
+// for MoE (docs/ROADMAP.md:39, "contiguous / masked layouts"); this is the
+// contiguous layout on the GEMM above.  The activation rows are sorted by
+// expert: expert e owns rows [expert_offsets[e], expert_offsets[e+1]).
+//   a_q: [m, k] E4M3, a_scales: [m, k/128] fp32 (as for the GEMM)
+//   b_q: [num_experts, n, k] E4M3, b_scales: [num_experts, ceil(n/128), k/128]
+//   expert_offsets: device int32 [num_experts + 1], non-decreasing, [0] = 0,
+//                   [num_experts] = m (values are clamped to [0, m])
+//   C:   [m, n] in out_dt; row r = A[r] x B[e]^T for the expert e owning r
+// Shape checks and diagnostics as for the GEMM (m = 0 is a no-op).
+void w8a8_block_fp8_grouped_gemm(void* c, const void* a_q, const void* a_scales,
+                                 const void* b_q, const void* b_scales,
+                                 const void* expert_offsets, int64_t m, int64_t n, int64_t k,
+                                 int64_t num_experts, int group_size = 128, int block_n = 128,
+                                 dtype out_dt = dtype::bf16, void* stream = nullptr);
+
 }  // namespace inferop

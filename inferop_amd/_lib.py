@@ -36,10 +36,15 @@ C_API = [
     ("inferop_silu_and_mul_quant_fp8", ctypes.c_int, [_vp, _vp, _vp, _i32, _i64, _i64, _i32, _vp]),
     ("inferop_fused_add_rmsnorm_quant_fp8", ctypes.c_int,
      [_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, ctypes.c_float, _i32, _vp]),
+    ("inferop_w8a8_block_fp8_grouped_gemm", ctypes.c_int,
+     [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _vp]),
     ("inferop_gemm_num_configs", ctypes.c_int, []),
     ("inferop_gemm_config_name", ctypes.c_char_p, [ctypes.c_int]),
     ("inferop_w8a8_block_fp8_gemm_config", ctypes.c_int,
      [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _i32, _vp]),
+    ("inferop_w8a8_block_fp8_grouped_gemm_config", ctypes.c_int,
+     [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i32, _vp]),
+    ("inferop_grouped_gemm_select", ctypes.c_int, [_i64, _i64, _i64, _i64, _vp]),
     ("inferop_gemm_select", ctypes.c_int,
      [_i64, _i64, _i64, ctypes.POINTER(_i32), ctypes.POINTER(_i32)]),
     ("inferop_selftest_fp8_codec", ctypes.c_int, [_u64, _u64, _vp, _vp]),

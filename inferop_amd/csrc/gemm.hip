@@ -65,6 +65,10 @@ struct GemmArgs {
   int* counters;  // split-K arrival counters, one per output tile
   int m, n, k;
   int vec_ok;  // C rows can take 4-element vector stores (N % 4 == 0, C aligned)
+  // grouped (MoE expert) GEMM: A's rows sorted by expert, expert e owning rows
+  // [offsets[e], offsets[e+1]); B and its scales hold `experts` matrices
+  const int* offsets;
+  int experts;
 };
 
 // Raw buffer resource over `bytes` bytes at base (stride 0; dword3 selects a
@@ -678,7 +682,49 @@ __device__ __forceinline__ void stage_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <int BN, int BM, int WN, int WM, int STAGES, int OUT_DT>
+// Grouped mode (GROUPED): grid x enumerates (N tile, virtual M tile) with
+// tiles_n * (ceil(M/BM) + experts) entries, enough for every expert's
+// ceil(rows/BM) M tiles.  A workgroup finds its expert by a prefix sum of the
+// experts' tile counts (read from the device offsets, clamped to [0, M] so any
+// offsets stay in bounds) and exits if its virtual tile is past the last one.
+// Its rows are the expert's [r0, r1) slice of that tile; B and the weight
+// scales are the expert's; rows past r1 read as zeros and are not stored.
+template <int BM>
+__device__ __forceinline__ bool grouped_tile(const GemmArgs& a, int tmv, int lane, int* e_out,
+                                             int* r0_out, int* r1_out) {
+  const int M = a.m, E = a.experts;
+  int cum = 0;
+  for (int c0 = 0; c0 < E; c0 += 64) {
+    const int ei = c0 + lane;
+    int lo = 0, hi = 0, cnt = 0;
+    if (ei < E) {
+      lo = min(max(a.offsets[ei], 0), M);
+      hi = min(max(a.offsets[ei + 1], lo), M);
+      cnt = (hi - lo + BM - 1) / BM;
+    }
+    int incl = cnt;  // inclusive prefix sum over the wave's 64 experts
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int v = __shfl_up(incl, d);
+      if (lane >= d) incl += v;
+    }
+    const int total = __shfl(incl, 63);
+    if (tmv < cum + total) {
+      const unsigned long long hit = __ballot(cum + incl > tmv);
+      const int l = __builtin_ctzll(hit);
+      const int before = cum + __shfl(incl - cnt, l);
+      const int r0 = __shfl(lo, l) + (tmv - before) * BM;
+      *e_out = __builtin_amdgcn_readfirstlane(c0 + l);
+      *r0_out = __builtin_amdgcn_readfirstlane(r0);
+      *r1_out = __builtin_amdgcn_readfirstlane(min(r0 + BM, __shfl(hi, l)));
+      return true;
+    }
+    cum += total;
+  }
+  return false;
+}
+
+template <int BN, int BM, int WN, int WM, int STAGES, int OUT_DT, bool GROUPED = false>
 __global__ __launch_bounds__(64 * WN * WM) void gemm_prefill_kernel(GemmArgs a) {
   constexpr int NW = WN * WM;
   constexpr int TN = BN / WN, TM = BM / WM;
@@ -728,17 +774,34 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_prefill_kernel(GemmArgs a) 
   const int L = xcd_contiguous((int)(blockIdx.y * gridDim.x + blockIdx.x), (int)(gridDim.x * gridDim.y));
   const int tile = L % (int)gridDim.x;
   int tn, tm;
-  tile_of(tile, tiles_n, tiles_m, &tn, &tm);
-  const int n0 = tn * BN, m0 = tm * BM;
+  // mend: end of the tile's rows; bq/bs: the weights (the expert's, grouped)
+  int n0, m0, mend;
+  const uint8_t* bq = a.bq;
+  const float* bs = a.bs;
+  if constexpr (GROUPED) {
+    int e, r0, r1;
+    if (!grouped_tile<BM>(a, tile / tiles_n, lane, &e, &r0, &r1)) return;
+    tn = tile % tiles_n;
+    n0 = tn * BN;
+    m0 = r0;
+    mend = r1;
+    bq += (int64_t)e * N * K;
+    bs += (int64_t)e * NB * KG;
+  } else {
+    tile_of(tile, tiles_n, tiles_m, &tn, &tm);
+    n0 = tn * BN;
+    m0 = tm * BM;
+    mend = M;
+  }
   // split-K: split z covers a contiguous range of scale groups
   const int split = gridDim.y, z = L / (int)gridDim.x;
   const int gb = (int)((int64_t)z * KG / split), ge = (int)((int64_t)(z + 1) * KG / split);
   const int NG = ge - gb;
   // tile buffers: rows past the last row of A or B read as zeros
-  const int nrows = min(BN, N - n0), mrows = min(BM, M - m0);
-  const __amdgpu_buffer_rsrc_t rB = make_rsrc(a.bq + (int64_t)n0 * K, (uint32_t)(nrows * K));
+  const int nrows = min(BN, N - n0), mrows = min(BM, mend - m0);
+  const __amdgpu_buffer_rsrc_t rB = make_rsrc(bq + (int64_t)n0 * K, (uint32_t)(nrows * K));
   const __amdgpu_buffer_rsrc_t rA = make_rsrc(a.aq + (int64_t)m0 * K, (uint32_t)(mrows * K));
-  const int mlast = M - 1 - m0;  // last valid row inside the tile
+  const int mlast = mend - 1 - m0;  // last valid row inside the tile
 
   // direct-to-LDS slots: wave instruction r covers rows 8*(wave + r*NW) .. +8;
   // lane -> row + (lane >> 3), chunk (lane & 7) ^ (lane >> 3).  The per-lane
@@ -761,7 +824,7 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_prefill_kernel(GemmArgs a) 
     // lanes 0..kSbBlocks-1 fetch the weight scales of the tile's blocks
     constexpr int kSbBlocks = BN >= 128 ? BN / 128 : 1;  // weight blocks the tile spans
     const int nb = min((n0 >> 7) + min(lane, kSbBlocks - 1), NB - 1);
-    scale_src = a.bs + (int64_t)nb * KG;
+    scale_src = bs + (int64_t)nb * KG;
     scale_dst = kOffSB;
   }
 
@@ -847,7 +910,7 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_prefill_kernel(GemmArgs a) 
     for (int i = 0; i < SN; ++i)
 #pragma unroll
       for (int j = 0; j < SM; ++j) part[i * SM + j] = acc[i][j];
-    auto valid = [&](int q) { return m0 + wm * TM + 16 * (q % SM) + rsub < M; };
+    auto valid = [&](int q) { return m0 + wm * TM + 16 * (q % SM) + rsub < mend; };
     if (!splitk_fixup<SN * SM>(a, part, split, z, tile, (int64_t)gridDim.x,
                                NW * SN * SM, wave * SN * SM, lane, valid))
       return;
@@ -861,9 +924,10 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_prefill_kernel(GemmArgs a) 
 #pragma unroll
     for (int i = 0; i < SN; ++i)
 #pragma unroll
-      for (int j = 0; j < SM; ++j)
-        store_out4<OUT_DT>(a, m0 + wm * TM + 16 * j + rsub, n0 + wn * TN + 16 * i + 4 * c0,
-                           acc[i][j]);
+      for (int j = 0; j < SM; ++j) {
+        const int m = m0 + wm * TM + 16 * j + rsub;
+        if (m < mend) store_out4<OUT_DT>(a, m, n0 + wn * TN + 16 * i + 4 * c0, acc[i][j]);
+      }
   } else {
     // 16-bit outputs leave through LDS: each lane's four consecutive outputs
     // go to the C tile in LDS (rows padded by 8 bytes so the 16 rows of a
@@ -894,7 +958,7 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_prefill_kernel(GemmArgs a) 
     for (int idx = threadIdx.x; idx < BM * kChunks; idx += 64 * NW) {
       const int ml = idx / kChunks, cc = idx % kChunks;
       const int m = m0 + ml, n = n0 + cc * 8;
-      if (m >= M || n >= N) continue;
+      if (m >= mend || n >= N) continue;
       const uint8_t* src = crow(ml) + cc * 16;
       OT* dst = C + (int64_t)m * N + n;
       if (vec && n + 7 < N) {
@@ -1201,9 +1265,10 @@ struct CfgEntry {
   int bn, bm, waves;
   const char* name;
   KernelFn fn[3];  // [out_dt index]
-  // wide decode only: the same configuration without the scale preload, for
-  // more than wide_scale_cap(MT) groups per wave
-  KernelFn fn_long[3];
+  // tiled (kind 2): the grouped-expert variant, where built (else null);
+  // wide decode (kind 4): the variant without the scale preload, for more
+  // than wide_scale_cap(MT) groups per wave
+  KernelFn fn_alt[3];
 };
 
 #define DECODE_CFG(MT, WK, U, NAME)                                                           \
@@ -1220,6 +1285,18 @@ struct CfgEntry {
     gemm_prefill_kernel<BN, BM, WN, WM, ST, kFp16>,                                            \
     gemm_prefill_kernel<BN, BM, WN, WM, ST, kBf16>}}
 
+#define PREFILL_GROUPED_CFG(BN, BM, WN, WM, ST, NAME)                                         \
+  {2,                                                                                          \
+   BN,                                                                                         \
+   BM,                                                                                         \
+   WN * WM,                                                                                    \
+   NAME,                                                                                       \
+   {gemm_prefill_kernel<BN, BM, WN, WM, ST, kFp32>,                                            \
+    gemm_prefill_kernel<BN, BM, WN, WM, ST, kFp16>,                                            \
+    gemm_prefill_kernel<BN, BM, WN, WM, ST, kBf16>},                                           \
+   {gemm_prefill_kernel<BN, BM, WN, WM, ST, kFp32, true>,                                      \
+    gemm_prefill_kernel<BN, BM, WN, WM, ST, kFp16, true>,                                      \
+    gemm_prefill_kernel<BN, BM, WN, WM, ST, kBf16, true>}}
 #define DECODE_WIDE_CFG(MT, WK, UW, UA, NAME)                                                  \
   {4,                                                                                          \
    16,                                                                                         \
@@ -1246,12 +1323,12 @@ const CfgEntry kCfgs[] = {
     DECODE_CFG(4, 4, 2, "dec_m64_k4_u2"),
     PREFILL_CFG(256, 128, 4, 2, 3, "pre_n256_m128_w8_s3"),
     PREFILL_CFG(128, 256, 2, 4, 3, "pre_n128_m256_w8_s3"),
-    PREFILL_CFG(128, 128, 2, 2, 2, "pre_n128_m128_w4_s2"),
+    PREFILL_GROUPED_CFG(128, 128, 2, 2, 2, "pre_n128_m128_w4_s2"),
     PREFILL_CFG(128, 128, 2, 2, 4, "pre_n128_m128_w4_s4"),
     PREFILL_CFG(256, 256, 2, 4, 2, "pre_n256_m256_w8_s2"),
-    PREFILL_CFG(128, 64, 8, 1, 4, "pre_n128_m64_w8_s4"),
-    PREFILL_CFG(128, 32, 8, 1, 4, "pre_n128_m32_w8_s4"),
-    PREFILL_CFG(128, 16, 8, 1, 4, "pre_n128_m16_w8_s4"),
+    PREFILL_GROUPED_CFG(128, 64, 8, 1, 4, "pre_n128_m64_w8_s4"),
+    PREFILL_GROUPED_CFG(128, 32, 8, 1, 4, "pre_n128_m32_w8_s4"),
+    PREFILL_GROUPED_CFG(128, 16, 8, 1, 4, "pre_n128_m16_w8_s4"),
     PREFILL_CFG(64, 64, 4, 1, 4, "pre_n64_m64_w4_s4"),
     PREFILL_CFG(128, 64, 8, 1, 3, "pre_n128_m64_w8_s3"),
     DECODE_LDS_CFG(2, 4, "decl_k2_u4"),
@@ -1372,6 +1449,7 @@ extern "C" int inferop_hip_gemm_config_info(int32_t cfg, inferop_gemm_cfg_info* 
   info->waves = kCfgs[cfg].waves;
   info->kind = kCfgs[cfg].kind;
   info->name = kCfgs[cfg].name;
+  info->grouped = kCfgs[cfg].kind == 2 && kCfgs[cfg].fn_alt[0] != nullptr;
   return hipSuccess;
 }
 
@@ -1414,7 +1492,7 @@ extern "C" int inferop_hip_gemm_w8a8_block(void* c, const uint8_t* a_q, const fl
     if ((int64_t)cf.bm * k > 0x7FFFFFFF) return hipErrorInvalidValue;
     if (tn > 0x7FFFFFFF || tm > 65535) return hipErrorInvalidConfiguration;
     const int64_t per_wave = (kg + cf.waves - 1) / cf.waves;
-    const KernelFn fn = per_wave <= wide_scale_cap(cf.bm / 16) ? cf.fn[di] : cf.fn_long[di];
+    const KernelFn fn = per_wave <= wide_scale_cap(cf.bm / 16) ? cf.fn[di] : cf.fn_alt[di];
     hipLaunchKernelGGL(fn, dim3((unsigned)tn, (unsigned)tm), dim3(64 * cf.waves), 0, st, args);
   } else if (cf.kind == 3) {
     // persistent: whole tiles (split_k is ignored), an even number of scale
@@ -1443,5 +1521,35 @@ extern "C" int inferop_hip_gemm_w8a8_block(void* c, const uint8_t* a_q, const fl
     hipLaunchKernelGGL(cf.fn[di], dim3((unsigned)tiles, (unsigned)split), dim3(64 * cf.waves), 0,
                        st, args);
   }
+  return hipGetLastError();
+}
+
+extern "C" int inferop_hip_gemm_w8a8_block_grouped(void* c, const uint8_t* a_q,
+                                                   const float* a_scales, const uint8_t* b_q,
+                                                   const float* b_scales, const int32_t* offsets,
+                                                   int64_t m, int64_t n, int64_t k,
+                                                   int64_t experts, int32_t out_dt, int32_t cfg,
+                                                   void* stream) {
+  const int di = dt_index(out_dt);
+  if (di < 0 || cfg < 0 || cfg >= kNumCfgs) return hipErrorInvalidValue;
+  const CfgEntry& cf = kCfgs[cfg];
+  if (cf.kind != 2 || !cf.fn_alt[di]) return hipErrorInvalidValue;
+  if (m < 0 || n <= 0 || k <= 0 || k % 128 != 0 || experts <= 0) return hipErrorInvalidValue;
+  if (m == 0) return hipSuccess;
+  if (m > 0x7FFFFFFF || n > 0x7FFFFFFF || k > 0x7FFFFFFF || experts > 0x7FFFFFFF)
+    return hipErrorInvalidValue;
+  // tile rows are addressed with 32-bit buffer offsets
+  if ((int64_t)(cf.bn > cf.bm ? cf.bn : cf.bm) * k > 0x7FFFFFFF) return hipErrorInvalidValue;
+  // every expert's M tiles fit in ceil(m / BM) + experts virtual tiles
+  const int64_t tn = (n + cf.bn - 1) / cf.bn;
+  const int64_t tmv = (m + cf.bm - 1) / cf.bm + experts;
+  if (tn * tmv > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int out_bytes = out_dt == kFp32 ? 4 : 2;
+  const int vec_ok = (n % 4 == 0) && ((uintptr_t)c % (size_t)(4 * out_bytes) == 0);
+  GemmArgs args{c,       a_q,    a_scales, b_q,    b_scales, nullptr,
+                nullptr, (int)m, (int)n,   (int)k, vec_ok,   offsets, (int)experts};
+  hipLaunchKernelGGL(cf.fn_alt[di], dim3((unsigned)(tn * tmv), 1u), dim3(64 * cf.waves), 0, st,
+                     args);
   return hipGetLastError();
 }

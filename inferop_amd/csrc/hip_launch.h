@@ -61,6 +61,7 @@ typedef struct {
                      4 = wide decode: a weight stripe over all of K with bm activation
                          rows (split_k ignored) */
   const char* name;
+  int32_t grouped; /* kind 2: has a grouped-expert variant */
 } inferop_gemm_cfg_info;
 
 int inferop_hip_gemm_num_configs(void);
@@ -69,6 +70,17 @@ int inferop_hip_gemm_w8a8_block(void* c, const uint8_t* a_q, const float* a_scal
                                 const uint8_t* b_q, const float* b_scales, int64_t m, int64_t n,
                                 int64_t k, int32_t out_dt, const inferop_gemm_launch* launch,
                                 void* stream);
+
+/* Grouped (MoE expert) GEMM, contiguous layout: A [m, k] rows sorted by
+ * expert, expert e owning rows [offsets[e], offsets[e+1]) (offsets: device
+ * int32 [experts + 1], clamped to [0, m] on the device); B [experts, n, k],
+ * b_scales [experts, ceil(n/128), k/128]; C [m, n].  cfg must be a tiled
+ * configuration with a grouped variant (inferop_gemm_cfg_info.grouped). */
+int inferop_hip_gemm_w8a8_block_grouped(void* c, const uint8_t* a_q, const float* a_scales,
+                                        const uint8_t* b_q, const float* b_scales,
+                                        const int32_t* offsets, int64_t m, int64_t n, int64_t k,
+                                        int64_t experts, int32_t out_dt, int32_t cfg,
+                                        void* stream);
 
 /* ---- device self-test of the E4M3 conversions used by the fast paths ----
  * counts[0]: fp32 patterns in [lo, hi) inside the quantizer fast-path domain

@@ -330,6 +330,54 @@ int gemm_impl(void* c, const void* a_q, const void* a_scales, const void* b_q,
   return gemm_launch(c, a_q, a_scales, b_q, b_scales, m, n, k, out_dt, ch.cfg, ch.split, stream);
 }
 
+// Grouped (MoE expert) GEMM, contiguous layout.  One M tile height for all
+// experts, from the mean rows per expert: HBM-bound while experts get few
+// rows (a tile reads its expert's whole weight slice whatever its rows), so
+// the tile height follows the rows to keep the MFMA and LDS work near what
+// the rows need; 128x128 once experts average about a tile of rows.
+int32_t select_grouped(int64_t m, int64_t num_experts) {
+  const int64_t avg = m / (num_experts > 0 ? num_experts : 1);
+  if (avg >= 96) return kPreN128M128S2;
+  if (avg >= 40) return kPreN128M64S4;
+  if (avg >= 20) return kPreN128M32S4;
+  return kPreN128M16S4;
+}
+
+bool grouped_shape_ok(int64_t m, int64_t n, int64_t k, int64_t experts, int32_t group_size,
+                      int32_t block_n) {
+  if (group_size != 128 || block_n != 128 || k <= 0 || k % 128 != 0 || m < 0 || n <= 0 ||
+      experts <= 0 || experts > 0x7FFFFFFF) {
+    std::fprintf(stderr,
+                 "[inferop] w8a8_block_fp8_grouped_gemm: unsupported shape (m=%lld n=%lld k=%lld "
+                 "experts=%lld gs=%d bn=%d); requires gs=bn=128, k%%128==0, experts>=1\n",
+                 (long long)m, (long long)n, (long long)k, (long long)experts, group_size,
+                 block_n);
+    return false;
+  }
+  return true;
+}
+
+int grouped_launch(void* c, const void* a_q, const void* a_scales, const void* b_q,
+                   const void* b_scales, const void* offsets, int64_t m, int64_t n, int64_t k,
+                   int64_t experts, int32_t out_dt, int32_t cfg, void* stream) {
+  return status_of_hip(inferop_hip_gemm_w8a8_block_grouped(
+      c, static_cast<const uint8_t*>(a_q), static_cast<const float*>(a_scales),
+      static_cast<const uint8_t*>(b_q), static_cast<const float*>(b_scales),
+      static_cast<const int32_t*>(offsets), m, n, k, experts, out_dt, cfg, stream));
+}
+
+int grouped_impl(void* c, const void* a_q, const void* a_scales, const void* b_q,
+                 const void* b_scales, const void* offsets, int64_t m, int64_t n, int64_t k,
+                 int64_t experts, int32_t group_size, int32_t block_n, int32_t out_dt,
+                 void* stream) {
+  if (!grouped_shape_ok(m, n, k, experts, group_size, block_n)) return INFEROP_ERR_SHAPE;
+  if (!valid_input_dtype(out_dt)) return INFEROP_ERR_DTYPE;
+  if (m == 0) return INFEROP_OK;
+  if (!gemm_device()) return INFEROP_ERR_DEVICE;
+  return grouped_launch(c, a_q, a_scales, b_q, b_scales, offsets, m, n, k, experts, out_dt,
+                        select_grouped(m, experts), stream);
+}
+
 }  // namespace
 
 // ---- ops.h --------------------------------------------------------------------
@@ -368,6 +416,15 @@ void w8a8_block_fp8_gemm(void* c, const void* a_q, const void* a_scales, const v
                          int block_n, dtype out_dt, void* stream) {
   (void)gemm_impl(c, a_q, a_scales, b_q, b_scales, m, n, k, group_size, block_n,
                   int32_t(out_dt), stream);
+}
+
+void w8a8_block_fp8_grouped_gemm(void* c, const void* a_q, const void* a_scales,
+                                 const void* b_q, const void* b_scales,
+                                 const void* expert_offsets, int64_t m, int64_t n, int64_t k,
+                                 int64_t num_experts, int group_size, int block_n, dtype out_dt,
+                                 void* stream) {
+  (void)grouped_impl(c, a_q, a_scales, b_q, b_scales, expert_offsets, m, n, k, num_experts,
+                     group_size, block_n, int32_t(out_dt), stream);
 }
 
 void topk_softmax(int32_t* topk_ids, void* topk_weights, const void* logits, int tokens,
@@ -482,6 +539,40 @@ extern "C" int inferop_w8a8_block_fp8_gemm_config(void* c, const void* a_q, cons
   if (info.kind == 3 && (k / 128) % 2 != 0) return INFEROP_ERR_ARGUMENT;
   if (!gemm_device()) return INFEROP_ERR_DEVICE;
   return gemm_launch(c, a_q, a_scales, b_q, b_scales, m, n, k, out_dt, config, split_k, stream);
+}
+
+extern "C" int inferop_w8a8_block_fp8_grouped_gemm(void* c, const void* a_q, const void* a_scales,
+                                                   const void* b_q, const void* b_scales,
+                                                   const int32_t* expert_offsets, int64_t m,
+                                                   int64_t n, int64_t k, int64_t num_experts,
+                                                   int32_t group_size, int32_t block_n,
+                                                   int32_t out_dt, void* stream) {
+  return grouped_impl(c, a_q, a_scales, b_q, b_scales, expert_offsets, m, n, k, num_experts,
+                      group_size, block_n, out_dt, stream);
+}
+
+extern "C" int inferop_w8a8_block_fp8_grouped_gemm_config(
+    void* c, const void* a_q, const void* a_scales, const void* b_q, const void* b_scales,
+    const int32_t* expert_offsets, int64_t m, int64_t n, int64_t k, int64_t num_experts,
+    int32_t out_dt, int32_t config, void* stream) {
+  if (!grouped_shape_ok(m, n, k, num_experts, 128, 128)) return INFEROP_ERR_SHAPE;
+  if (!valid_input_dtype(out_dt)) return INFEROP_ERR_DTYPE;
+  inferop_gemm_cfg_info info{};
+  if (config < 0 || config >= inferop_hip_gemm_num_configs() ||
+      inferop_hip_gemm_config_info(config, &info) != 0 || !info.grouped)
+    return INFEROP_ERR_ARGUMENT;
+  if (m == 0) return INFEROP_OK;
+  if (!gemm_device()) return INFEROP_ERR_DEVICE;
+  return grouped_launch(c, a_q, a_scales, b_q, b_scales, expert_offsets, m, n, k, num_experts,
+                        out_dt, config, stream);
+}
+
+extern "C" int inferop_grouped_gemm_select(int64_t m, int64_t n, int64_t k, int64_t num_experts,
+                                           int32_t* config) {
+  if (m < 0 || n <= 0 || k <= 0 || k % 128 != 0 || num_experts <= 0 || !config)
+    return INFEROP_ERR_ARGUMENT;
+  *config = select_grouped(m, num_experts);
+  return INFEROP_OK;
 }
 
 extern "C" int inferop_gemm_select(int64_t m, int64_t n, int64_t k, int32_t* config,

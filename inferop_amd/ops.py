@@ -119,6 +119,16 @@ def quant_fp8_weight_block(b_q, b_scales, w, dt, n: int, k: int, group_size: int
         _ptr(b_q), _ptr(b_scales), _ptr(w), int(dt), n, k, group_size, block_n, _stream(stream))
 
 
+# ---- extension: grouped GEMM over MoE experts, contiguous layout (the
+# reference's roadmap item, docs/ROADMAP.md:39; no counterpart in its ops.h) ----
+def w8a8_block_fp8_grouped_gemm(c, a_q, a_scales, b_q, b_scales, expert_offsets, m: int, n: int,
+                                k: int, num_experts: int, group_size: int = 128,
+                                block_n: int = 128, out_dt=dtype.bf16, stream=None) -> int:
+    return lib().inferop_w8a8_block_fp8_grouped_gemm(
+        _ptr(c), _ptr(a_q), _ptr(a_scales), _ptr(b_q), _ptr(b_scales), _ptr(expert_offsets), m, n,
+        k, num_experts, group_size, block_n, int(out_dt), _stream(stream))
+
+
 # ---- extension: producers fused with the quantizer (the reference runs
 # silu_and_mul / fused_add_rmsnorm, ops.h:33-55, then quant_fp8_per_token_group) ----
 def silu_and_mul_quant_fp8(q, scales, gate_up, dt, tokens: int, d: int, group_size: int = 128,
@@ -156,6 +166,22 @@ def w8a8_block_fp8_gemm_config(c, a_q, a_scales, b_q, b_scales, m: int, n: int, 
     return lib().inferop_w8a8_block_fp8_gemm_config(
         _ptr(c), _ptr(a_q), _ptr(a_scales), _ptr(b_q), _ptr(b_scales), m, n, k, int(out_dt),
         config, split_k, _stream(stream))
+
+
+def w8a8_block_fp8_grouped_gemm_config(c, a_q, a_scales, b_q, b_scales, expert_offsets, m: int,
+                                       n: int, k: int, num_experts: int, out_dt, config: int,
+                                       stream=None) -> int:
+    return lib().inferop_w8a8_block_fp8_grouped_gemm_config(
+        _ptr(c), _ptr(a_q), _ptr(a_scales), _ptr(b_q), _ptr(b_scales), _ptr(expert_offsets), m, n,
+        k, num_experts, int(out_dt), config, _stream(stream))
+
+
+def grouped_gemm_select(m: int, n: int, k: int, num_experts: int) -> int:
+    cfg = ctypes.c_int32()
+    st = lib().inferop_grouped_gemm_select(m, n, k, num_experts, ctypes.byref(cfg))
+    if st != Status.OK:
+        raise InferopError(st, "grouped_gemm_select")
+    return cfg.value
 
 
 def selftest_fp8_codec(counts, lo: int = 0, hi: int = 1 << 32, stream=None) -> int:

@@ -197,6 +197,31 @@ def test_gemm_selection_covers_configs():
     assert names[inferop_amd.gemm_select(4096, 7168, 16384 + 128)[0]] == "pre_n256_m256_w8_s2"
 
 
+def test_grouped_gemm_host_checks():
+    # checked before any device work: shape and dtype errors, the m = 0
+    # no-op, forced configurations without a grouped variant, and the tile
+    # height chosen from the mean rows per expert
+    S = inferop_amd.Status
+    g = inferop_amd.w8a8_block_fp8_grouped_gemm
+    assert g(0, 0, 0, 0, 0, 0, 16, 512, 1000, 8) == S.ERR_SHAPE
+    assert g(0, 0, 0, 0, 0, 0, 16, 512, 1024, 0) == S.ERR_SHAPE
+    assert g(0, 0, 0, 0, 0, 0, -1, 512, 1024, 8) == S.ERR_SHAPE
+    assert g(0, 0, 0, 0, 0, 0, 16, 512, 1024, 8, group_size=64) == S.ERR_SHAPE
+    assert g(0, 0, 0, 0, 0, 0, 16, 512, 1024, 8, out_dt=inferop_amd.dtype.fp8_e4m3) == S.ERR_DTYPE
+    assert g(0, 0, 0, 0, 0, 0, 0, 512, 1024, 8) == S.OK
+    names = [inferop_amd.gemm_config_name(i) for i in range(inferop_amd.gemm_num_configs())]
+    gc = inferop_amd.w8a8_block_fp8_grouped_gemm_config
+    for i, name in enumerate(names):
+        if name not in ("pre_n128_m128_w4_s2", "pre_n128_m64_w8_s4", "pre_n128_m32_w8_s4",
+                        "pre_n128_m16_w8_s4"):
+            assert gc(0, 0, 0, 0, 0, 0, 16, 512, 1024, 8, inferop_amd.dtype.bf16, i) == \
+                S.ERR_ARGUMENT, name
+    sel = lambda m, e: names[inferop_amd.grouped_gemm_select(m, 4096, 7168, e)]
+    assert sel(64 * 8, 256) == "pre_n128_m16_w8_s4"
+    assert sel(32 * 256, 256) == "pre_n128_m32_w8_s4"
+    assert sel(4096 * 8, 256) == "pre_n128_m128_w4_s2"
+
+
 def test_persistent_config_rejects_odd_group_count():
     # checked before any device work: the persistent kernels need K / 128 even
     S = inferop_amd.Status
