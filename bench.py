@@ -10,9 +10,12 @@ the 256 MB Infinity Cache cannot serve them.  `value` is the step's
 algorithmic HBM bytes divided by its wall time (GB/s).
 
 Also reported: the prefill GEMM (configs[2], M = 4096) in TFLOPS against the
-5.0 PFLOPS dense-FP8 peak, the quantizer on large inputs in GB/s, and a CPU
-baseline (the reference's own CPU golden code, or the oracle restatement,
-timed single-threaded on this host over the same decode workload).
+5.0 PFLOPS dense-FP8 peak (with the platform's row-wise FP8 GEMM on the same
+bytes as a reference point), the quantizer, weight quantizer and fused
+producers on large inputs in GB/s, MoE routing, the grouped GEMM over MoE
+experts (decode- and prefill-sized routings), and a CPU baseline (the
+reference's own CPU golden code, or the oracle restatement, timed
+single-threaded on this host over the same decode workload).
 Per-kernel durations come from HIP events on the launch stream around graph
 replays of back-to-back launches of one kernel.
 
@@ -120,6 +123,7 @@ def main():
                                    "multi-GPU component here (sharding is described in "
                                    "DESIGN.md); run with --gpus 1"}))
         sys.exit(2)
+    import numpy as np
     import torch
 
     import inferop_amd as ia
@@ -429,6 +433,46 @@ def main():
             tres.append({"tokens": tok, "experts": 256, "topk": 8, "us": round(us, 2)})
             del lg, tid, twt, gt
         result["topk_softmax"] = {"shapes": tres}
+
+        # ---------------- grouped GEMM over MoE experts ----------------
+        # One GPU's share of a DeepSeek-V3-like MoE layer with 8-way expert
+        # parallelism: 32 local experts, gate/up projection (N = 2 x 2048,
+        # K = 7168), contiguous layout, rows per expert drawn from a uniform
+        # multinomial routing.  Decode: 64 token-expert rows (the call streams
+        # every expert's weights: GB/s of weight bytes); prefill: 4096 rows
+        # (TFLOP/s).  Two weight copies (1.9 GB) so neither cache holds them.
+        gres = []
+        ge_, gn, gk = 32, 4096, 7168
+        wsets = [(rand_fp8((ge_, gn, gk)), rand_scales((ge_, gn // 128, gk // 128)))
+                 for _ in range(2)]
+        for gm in (64, 4096):
+            sizes = np.random.default_rng(gm).multinomial(gm, np.ones(ge_) / ge_)
+            off = torch.tensor(np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32),
+                               device=dev)
+            gaq = rand_fp8((gm, gk))
+            gas = rand_scales((gm, gk // 128))
+            gc = torch.empty((gm, gn), dtype=torch.bfloat16, device=dev)
+
+            def fg(i, gm=gm, off=off, gaq=gaq, gas=gas, gc=gc):
+                bq, bs = wsets[i % 2]
+                st = ia.w8a8_block_fp8_grouped_gemm(gc, gaq, gas, bq, bs, off, gm, gn, gk, ge_,
+                                                    128, 128, DT.bf16, sp)
+                assert st == 0, st
+
+            gg = capture(lambda: [fg(i) for i in range(10)])
+            time_graphs([gg], 2)
+            us = time_graphs([gg], 5) / 10 * 1e3
+            wbytes = ge_ * gn * gk + 4 * ge_ * (gn // 128) * (gk // 128)
+            gbytes = wbytes + gm * gk + 4 * gm * (gk // 128) + 2 * gm * gn
+            gres.append({"rows": gm, "experts": ge_, "n": gn, "k": gk, "us": round(us, 2),
+                         "gbs": round(gbytes / (us * 1e-6) / 1e9, 1),
+                         "hbm_frac": round(gbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                         "tflops": round(2.0 * gm * gn * gk / (us * 1e-6) / 1e12, 1),
+                         "kernel": ia.gemm_config_name(ia.grouped_gemm_select(gm, gn, gk, ge_))})
+            del off, gaq, gas, gc, gg
+        del wsets
+        result["moe_grouped_gemm"] = {"shapes": gres, "peak_gbs": HBM_PEAK_GBS,
+                                      "peak_tflops": FP8_PEAK_TFLOPS}
 
         result["quant"] = {"shapes": qres, "peak_gbs": HBM_PEAK_GBS,
                            "roofline": {"bound": "hbm", "kernel": "per-token-group quantizer",

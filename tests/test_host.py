@@ -218,7 +218,8 @@ def test_grouped_gemm_host_checks():
                 S.ERR_ARGUMENT, name
     sel = lambda m, e: names[inferop_amd.grouped_gemm_select(m, 4096, 7168, e)]
     assert sel(64 * 8, 256) == "pre_n128_m16_w8_s4"
-    assert sel(32 * 256, 256) == "pre_n128_m32_w8_s4"
+    assert sel(20 * 256, 256) == "pre_n128_m32_w8_s4"
+    assert sel(32 * 256, 256) == "pre_n128_m128_w4_s2"
     assert sel(4096 * 8, 256) == "pre_n128_m128_w4_s2"
 
 
