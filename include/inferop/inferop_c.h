@@ -102,6 +102,17 @@ int inferop_w8a8_block_fp8_grouped_gemm(void* c, const void* a_q, const void* a_
                                         const int32_t* expert_offsets, int64_t m, int64_t n,
                                         int64_t k, int64_t num_experts, int32_t group_size,
                                         int32_t block_n, int32_t out_dt, void* stream);
+/* Masked layout, as inferop::w8a8_block_fp8_grouped_gemm_masked in ops.h:
+ * a_q [num_experts, max_m, k], masked_m device int32 [num_experts] valid rows
+ * per expert (clamped to [0, max_m]), c [num_experts, max_m, n] (rows past a
+ * count are not written); expected_m: tile-choice hint (<= 0: max_m).
+ * max_m = 0 returns INFEROP_OK without a launch. */
+int inferop_w8a8_block_fp8_grouped_gemm_masked(void* c, const void* a_q, const void* a_scales,
+                                               const void* b_q, const void* b_scales,
+                                               const int32_t* masked_m, int64_t max_m, int64_t n,
+                                               int64_t k, int64_t num_experts, int64_t expected_m,
+                                               int32_t group_size, int32_t block_n,
+                                               int32_t out_dt, void* stream);
 
 /* --- tuning and testing (no counterpart in the reference) ---
  * The GEMM with an explicit kernel configuration and split-K factor instead
@@ -126,6 +137,13 @@ int inferop_w8a8_block_fp8_grouped_gemm_config(void* c, const void* a_q, const v
                                                int32_t out_dt, int32_t config, void* stream);
 int inferop_grouped_gemm_select(int64_t m, int64_t n, int64_t k, int64_t num_experts,
                                 int32_t* config);
+int inferop_w8a8_block_fp8_grouped_gemm_masked_config(void* c, const void* a_q,
+                                                      const void* a_scales, const void* b_q,
+                                                      const void* b_scales,
+                                                      const int32_t* masked_m, int64_t max_m,
+                                                      int64_t n, int64_t k, int64_t num_experts,
+                                                      int32_t out_dt, int32_t config,
+                                                      void* stream);
 
 /* --- diagnostics (no counterpart in the reference) ---
  * Compares, on the current device, the hardware E4M3 conversions the fast

@@ -125,4 +125,19 @@ void w8a8_block_fp8_grouped_gemm(void* c, const void* a_q, const void* a_scales,
                                  int64_t num_experts, int group_size = 128, int block_n = 128,
                                  dtype out_dt = dtype::bf16, void* stream = nullptr);
 
+// The masked layout of the same GEMM (the roadmap's second layout): every
+// expert has a fixed block of max_m rows, of which masked_m[e] are valid, so
+// the call's shapes do not depend on the routing (graph capture of decode).
+//   a_q: [num_experts, max_m, k] E4M3, a_scales: [num_experts, max_m, k/128]
+//   masked_m: device int32 [num_experts] (clamped to [0, max_m])
+//   C:   [num_experts, max_m, n]; rows past an expert's count are not written
+// expected_m: typical valid rows per expert, a hint for the tile choice
+// (<= 0: max_m).  Shape checks as for the GEMM (max_m = 0 is a no-op).
+void w8a8_block_fp8_grouped_gemm_masked(void* c, const void* a_q, const void* a_scales,
+                                        const void* b_q, const void* b_scales,
+                                        const void* masked_m, int64_t max_m, int64_t n, int64_t k,
+                                        int64_t num_experts, int64_t expected_m = 0,
+                                        int group_size = 128, int block_n = 128,
+                                        dtype out_dt = dtype::bf16, void* stream = nullptr);
+
 }  // namespace inferop

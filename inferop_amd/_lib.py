@@ -38,6 +38,8 @@ C_API = [
      [_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, ctypes.c_float, _i32, _vp]),
     ("inferop_w8a8_block_fp8_grouped_gemm", ctypes.c_int,
      [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _vp]),
+    ("inferop_w8a8_block_fp8_grouped_gemm_masked", ctypes.c_int,
+     [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _vp]),
     ("inferop_gemm_num_configs", ctypes.c_int, []),
     ("inferop_gemm_config_name", ctypes.c_char_p, [ctypes.c_int]),
     ("inferop_w8a8_block_fp8_gemm_config", ctypes.c_int,
@@ -45,6 +47,8 @@ C_API = [
     ("inferop_w8a8_block_fp8_grouped_gemm_config", ctypes.c_int,
      [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i32, _vp]),
     ("inferop_grouped_gemm_select", ctypes.c_int, [_i64, _i64, _i64, _i64, _vp]),
+    ("inferop_w8a8_block_fp8_grouped_gemm_masked_config", ctypes.c_int,
+     [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i32, _vp]),
     ("inferop_gemm_select", ctypes.c_int,
      [_i64, _i64, _i64, ctypes.POINTER(_i32), ctypes.POINTER(_i32)]),
     ("inferop_selftest_fp8_codec", ctypes.c_int, [_u64, _u64, _vp, _vp]),

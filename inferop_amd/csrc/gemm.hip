@@ -65,10 +65,13 @@ struct GemmArgs {
   int* counters;  // split-K arrival counters, one per output tile
   int m, n, k;
   int vec_ok;  // C rows can take 4-element vector stores (N % 4 == 0, C aligned)
-  // grouped (MoE expert) GEMM: A's rows sorted by expert, expert e owning rows
-  // [offsets[e], offsets[e+1]); B and its scales hold `experts` matrices
+  // grouped (MoE expert) GEMM; B and its scales hold `experts` matrices.
+  // Contiguous layout (max_m == 0): A's rows sorted by expert, expert e owning
+  // rows [offsets[e], offsets[e+1]).  Masked layout (max_m > 0): expert e
+  // owns rows [e * max_m, e * max_m + offsets[e]) (offsets = valid counts).
   const int* offsets;
   int experts;
+  int max_m;
 };
 
 // Raw buffer resource over `bytes` bytes at base (stride 0; dword3 selects a
@@ -685,8 +688,9 @@ __device__ __forceinline__ void stage_barrier() {
 // Grouped mode (GROUPED): grid x enumerates (N tile, virtual M tile) with
 // tiles_n * (ceil(M/BM) + experts) entries, enough for every expert's
 // ceil(rows/BM) M tiles.  A workgroup finds its expert by a prefix sum of the
-// experts' tile counts (read from the device offsets, clamped to [0, M] so any
-// offsets stay in bounds) and exits if its virtual tile is past the last one.
+// experts' tile counts (read from the device offsets or counts, clamped so
+// that any values stay in bounds: offsets to [0, M], counts to [0, max_m]) and
+// exits if its virtual tile is past the last one.
 // Its rows are the expert's [r0, r1) slice of that tile; B and the weight
 // scales are the expert's; rows past r1 read as zeros and are not stored.
 template <int BM>
@@ -698,8 +702,13 @@ __device__ __forceinline__ bool grouped_tile(const GemmArgs& a, int tmv, int lan
     const int ei = c0 + lane;
     int lo = 0, hi = 0, cnt = 0;
     if (ei < E) {
-      lo = min(max(a.offsets[ei], 0), M);
-      hi = min(max(a.offsets[ei + 1], lo), M);
+      if (a.max_m > 0) {
+        lo = ei * a.max_m;
+        hi = lo + min(max(a.offsets[ei], 0), a.max_m);
+      } else {
+        lo = min(max(a.offsets[ei], 0), M);
+        hi = min(max(a.offsets[ei + 1], lo), M);
+      }
       cnt = (hi - lo + BM - 1) / BM;
     }
     int incl = cnt;  // inclusive prefix sum over the wave's 64 experts
@@ -1528,13 +1537,16 @@ extern "C" int inferop_hip_gemm_w8a8_block_grouped(void* c, const uint8_t* a_q,
                                                    const float* a_scales, const uint8_t* b_q,
                                                    const float* b_scales, const int32_t* offsets,
                                                    int64_t m, int64_t n, int64_t k,
-                                                   int64_t experts, int32_t out_dt, int32_t cfg,
-                                                   void* stream) {
+                                                   int64_t experts, int64_t max_m,
+                                                   int32_t out_dt, int32_t cfg, void* stream) {
   const int di = dt_index(out_dt);
   if (di < 0 || cfg < 0 || cfg >= kNumCfgs) return hipErrorInvalidValue;
   const CfgEntry& cf = kCfgs[cfg];
   if (cf.kind != 2 || !cf.fn_alt[di]) return hipErrorInvalidValue;
-  if (m < 0 || n <= 0 || k <= 0 || k % 128 != 0 || experts <= 0) return hipErrorInvalidValue;
+  if (m < 0 || n <= 0 || k <= 0 || k % 128 != 0 || experts <= 0 || max_m < 0)
+    return hipErrorInvalidValue;
+  // masked layout: m is the experts' max_m-row blocks end to end
+  if (max_m > 0 && m != experts * max_m) return hipErrorInvalidValue;
   if (m == 0) return hipSuccess;
   if (m > 0x7FFFFFFF || n > 0x7FFFFFFF || k > 0x7FFFFFFF || experts > 0x7FFFFFFF)
     return hipErrorInvalidValue;
@@ -1547,8 +1559,9 @@ extern "C" int inferop_hip_gemm_w8a8_block_grouped(void* c, const uint8_t* a_q,
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int out_bytes = out_dt == kFp32 ? 4 : 2;
   const int vec_ok = (n % 4 == 0) && ((uintptr_t)c % (size_t)(4 * out_bytes) == 0);
-  GemmArgs args{c,       a_q,    a_scales, b_q,    b_scales, nullptr,
-                nullptr, (int)m, (int)n,   (int)k, vec_ok,   offsets, (int)experts};
+  GemmArgs args{c,      a_q,    a_scales,     b_q,         b_scales,
+                nullptr, nullptr, (int)m,     (int)n,      (int)k,
+                vec_ok, offsets, (int)experts, (int)max_m};
   hipLaunchKernelGGL(cf.fn_alt[di], dim3((unsigned)(tn * tmv), 1u), dim3(64 * cf.waves), 0, st,
                      args);
   return hipGetLastError();

@@ -71,16 +71,20 @@ int inferop_hip_gemm_w8a8_block(void* c, const uint8_t* a_q, const float* a_scal
                                 int64_t k, int32_t out_dt, const inferop_gemm_launch* launch,
                                 void* stream);
 
-/* Grouped (MoE expert) GEMM, contiguous layout: A [m, k] rows sorted by
- * expert, expert e owning rows [offsets[e], offsets[e+1]) (offsets: device
- * int32 [experts + 1], clamped to [0, m] on the device); B [experts, n, k],
- * b_scales [experts, ceil(n/128), k/128]; C [m, n].  cfg must be a tiled
- * configuration with a grouped variant (inferop_gemm_cfg_info.grouped). */
+/* Grouped (MoE expert) GEMM; B [experts, n, k], b_scales [experts,
+ * ceil(n/128), k/128]; C [m, n]; cfg must be a tiled configuration with a
+ * grouped variant (inferop_gemm_cfg_info.grouped).
+ * max_m == 0, contiguous layout: A [m, k] rows sorted by expert, expert e
+ * owning rows [offsets[e], offsets[e+1]) (offsets: device int32
+ * [experts + 1], clamped to [0, m] on the device).
+ * max_m > 0, masked layout: m == experts * max_m, expert e owning rows
+ * [e * max_m, e * max_m + offsets[e]) (offsets: device int32 [experts] valid
+ * counts, clamped to [0, max_m]); other rows of C are not written. */
 int inferop_hip_gemm_w8a8_block_grouped(void* c, const uint8_t* a_q, const float* a_scales,
                                         const uint8_t* b_q, const float* b_scales,
                                         const int32_t* offsets, int64_t m, int64_t n, int64_t k,
-                                        int64_t experts, int32_t out_dt, int32_t cfg,
-                                        void* stream);
+                                        int64_t experts, int64_t max_m, int32_t out_dt,
+                                        int32_t cfg, void* stream);
 
 /* ---- device self-test of the E4M3 conversions used by the fast paths ----
  * counts[0]: fp32 patterns in [lo, hi) inside the quantizer fast-path domain

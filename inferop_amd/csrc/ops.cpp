@@ -360,11 +360,43 @@ bool grouped_shape_ok(int64_t m, int64_t n, int64_t k, int64_t experts, int32_t 
 
 int grouped_launch(void* c, const void* a_q, const void* a_scales, const void* b_q,
                    const void* b_scales, const void* offsets, int64_t m, int64_t n, int64_t k,
-                   int64_t experts, int32_t out_dt, int32_t cfg, void* stream) {
+                   int64_t experts, int64_t max_m, int32_t out_dt, int32_t cfg, void* stream) {
   return status_of_hip(inferop_hip_gemm_w8a8_block_grouped(
       c, static_cast<const uint8_t*>(a_q), static_cast<const float*>(a_scales),
       static_cast<const uint8_t*>(b_q), static_cast<const float*>(b_scales),
-      static_cast<const int32_t*>(offsets), m, n, k, experts, out_dt, cfg, stream));
+      static_cast<const int32_t*>(offsets), m, n, k, experts, max_m, out_dt, cfg, stream));
+}
+
+// Masked layout: experts x max_m rows (and C rows), counts on the device.
+bool masked_shape_ok(int64_t max_m, int64_t n, int64_t k, int64_t experts, int32_t group_size,
+                     int32_t block_n) {
+  if (group_size != 128 || block_n != 128 || k <= 0 || k % 128 != 0 || max_m < 0 || n <= 0 ||
+      experts <= 0 || experts > 0x7FFFFFFF || (max_m > 0 && experts > 0x7FFFFFFF / max_m)) {
+    std::fprintf(stderr,
+                 "[inferop] w8a8_block_fp8_grouped_gemm_masked: unsupported shape (max_m=%lld "
+                 "n=%lld k=%lld experts=%lld gs=%d bn=%d); requires gs=bn=128, k%%128==0, "
+                 "experts>=1, experts*max_m < 2^31\n",
+                 (long long)max_m, (long long)n, (long long)k, (long long)experts, group_size,
+                 block_n);
+    return false;
+  }
+  return true;
+}
+
+int masked_impl(void* c, const void* a_q, const void* a_scales, const void* b_q,
+                const void* b_scales, const void* masked_m, int64_t max_m, int64_t n, int64_t k,
+                int64_t experts, int64_t expected_m, int32_t group_size, int32_t block_n,
+                int32_t out_dt, int32_t cfg, void* stream) {
+  if (!masked_shape_ok(max_m, n, k, experts, group_size, block_n)) return INFEROP_ERR_SHAPE;
+  if (!valid_input_dtype(out_dt)) return INFEROP_ERR_DTYPE;
+  if (cfg < 0) {
+    const int64_t rows = expected_m > 0 ? (expected_m < max_m ? expected_m : max_m) : max_m;
+    cfg = select_grouped(rows * experts, experts);
+  }
+  if (max_m == 0) return INFEROP_OK;
+  if (!gemm_device()) return INFEROP_ERR_DEVICE;
+  return grouped_launch(c, a_q, a_scales, b_q, b_scales, masked_m, experts * max_m, n, k,
+                        experts, max_m, out_dt, cfg, stream);
 }
 
 int grouped_impl(void* c, const void* a_q, const void* a_scales, const void* b_q,
@@ -375,7 +407,7 @@ int grouped_impl(void* c, const void* a_q, const void* a_scales, const void* b_q
   if (!valid_input_dtype(out_dt)) return INFEROP_ERR_DTYPE;
   if (m == 0) return INFEROP_OK;
   if (!gemm_device()) return INFEROP_ERR_DEVICE;
-  return grouped_launch(c, a_q, a_scales, b_q, b_scales, offsets, m, n, k, experts, out_dt,
+  return grouped_launch(c, a_q, a_scales, b_q, b_scales, offsets, m, n, k, experts, 0, out_dt,
                         select_grouped(m, experts), stream);
 }
 
@@ -426,6 +458,15 @@ void w8a8_block_fp8_grouped_gemm(void* c, const void* a_q, const void* a_scales,
                                  void* stream) {
   (void)grouped_impl(c, a_q, a_scales, b_q, b_scales, expert_offsets, m, n, k, num_experts,
                      group_size, block_n, int32_t(out_dt), stream);
+}
+
+void w8a8_block_fp8_grouped_gemm_masked(void* c, const void* a_q, const void* a_scales,
+                                        const void* b_q, const void* b_scales,
+                                        const void* masked_m, int64_t max_m, int64_t n, int64_t k,
+                                        int64_t num_experts, int64_t expected_m, int group_size,
+                                        int block_n, dtype out_dt, void* stream) {
+  (void)masked_impl(c, a_q, a_scales, b_q, b_scales, masked_m, max_m, n, k, num_experts,
+                    expected_m, group_size, block_n, int32_t(out_dt), -1, stream);
 }
 
 void topk_softmax(int32_t* topk_ids, void* topk_weights, const void* logits, int tokens,
@@ -564,8 +605,28 @@ extern "C" int inferop_w8a8_block_fp8_grouped_gemm_config(
     return INFEROP_ERR_ARGUMENT;
   if (m == 0) return INFEROP_OK;
   if (!gemm_device()) return INFEROP_ERR_DEVICE;
-  return grouped_launch(c, a_q, a_scales, b_q, b_scales, expert_offsets, m, n, k, num_experts,
+  return grouped_launch(c, a_q, a_scales, b_q, b_scales, expert_offsets, m, n, k, num_experts, 0,
                         out_dt, config, stream);
+}
+
+extern "C" int inferop_w8a8_block_fp8_grouped_gemm_masked(
+    void* c, const void* a_q, const void* a_scales, const void* b_q, const void* b_scales,
+    const int32_t* masked_m, int64_t max_m, int64_t n, int64_t k, int64_t num_experts,
+    int64_t expected_m, int32_t group_size, int32_t block_n, int32_t out_dt, void* stream) {
+  return masked_impl(c, a_q, a_scales, b_q, b_scales, masked_m, max_m, n, k, num_experts,
+                     expected_m, group_size, block_n, out_dt, -1, stream);
+}
+
+extern "C" int inferop_w8a8_block_fp8_grouped_gemm_masked_config(
+    void* c, const void* a_q, const void* a_scales, const void* b_q, const void* b_scales,
+    const int32_t* masked_m, int64_t max_m, int64_t n, int64_t k, int64_t num_experts,
+    int32_t out_dt, int32_t config, void* stream) {
+  inferop_gemm_cfg_info info{};
+  if (config < 0 || config >= inferop_hip_gemm_num_configs() ||
+      inferop_hip_gemm_config_info(config, &info) != 0 || !info.grouped)
+    return INFEROP_ERR_ARGUMENT;
+  return masked_impl(c, a_q, a_scales, b_q, b_scales, masked_m, max_m, n, k, num_experts, 0, 128,
+                     128, out_dt, config, stream);
 }
 
 extern "C" int inferop_grouped_gemm_select(int64_t m, int64_t n, int64_t k, int64_t num_experts,

@@ -129,6 +129,15 @@ def w8a8_block_fp8_grouped_gemm(c, a_q, a_scales, b_q, b_scales, expert_offsets,
         k, num_experts, group_size, block_n, int(out_dt), _stream(stream))
 
 
+def w8a8_block_fp8_grouped_gemm_masked(c, a_q, a_scales, b_q, b_scales, masked_m, max_m: int,
+                                       n: int, k: int, num_experts: int, expected_m: int = 0,
+                                       group_size: int = 128, block_n: int = 128,
+                                       out_dt=dtype.bf16, stream=None) -> int:
+    return lib().inferop_w8a8_block_fp8_grouped_gemm_masked(
+        _ptr(c), _ptr(a_q), _ptr(a_scales), _ptr(b_q), _ptr(b_scales), _ptr(masked_m), max_m, n,
+        k, num_experts, expected_m, group_size, block_n, int(out_dt), _stream(stream))
+
+
 # ---- extension: producers fused with the quantizer (the reference runs
 # silu_and_mul / fused_add_rmsnorm, ops.h:33-55, then quant_fp8_per_token_group) ----
 def silu_and_mul_quant_fp8(q, scales, gate_up, dt, tokens: int, d: int, group_size: int = 128,
@@ -173,6 +182,14 @@ def w8a8_block_fp8_grouped_gemm_config(c, a_q, a_scales, b_q, b_scales, expert_o
                                        stream=None) -> int:
     return lib().inferop_w8a8_block_fp8_grouped_gemm_config(
         _ptr(c), _ptr(a_q), _ptr(a_scales), _ptr(b_q), _ptr(b_scales), _ptr(expert_offsets), m, n,
+        k, num_experts, int(out_dt), config, _stream(stream))
+
+
+def w8a8_block_fp8_grouped_gemm_masked_config(c, a_q, a_scales, b_q, b_scales, masked_m,
+                                              max_m: int, n: int, k: int, num_experts: int,
+                                              out_dt, config: int, stream=None) -> int:
+    return lib().inferop_w8a8_block_fp8_grouped_gemm_masked_config(
+        _ptr(c), _ptr(a_q), _ptr(a_scales), _ptr(b_q), _ptr(b_scales), _ptr(masked_m), max_m, n,
         k, num_experts, int(out_dt), config, _stream(stream))
 
 

@@ -162,3 +162,75 @@ def test_grouped_rejected_calls():
     assert g(c, 0, 0, 0, 0, 0, 4, 128, 256, 0) == S.ERR_SHAPE
     assert g(c, 0, 0, 0, 0, 0, 4, 128, 256, 4, out_dt=DT.fp8_e4m3) == S.ERR_DTYPE
     assert torch.all(c == 7.0)
+
+
+def _masked_inputs(counts, max_m, aq, as_, offsets):
+    """Scatter the contiguous layout's expert segments into the masked layout
+    [E, max_m, ...] (rows past a count: arbitrary bytes, never read as data)."""
+    e_n = len(counts)
+    k = aq.shape[1]
+    a3 = np.random.default_rng(7).integers(0, 0x7E, (e_n, max_m, k), dtype=np.uint8)
+    s3 = np.full((e_n, max_m, k // 128), 1.0, np.float32)
+    for e in range(e_n):
+        r0, r1 = int(offsets[e]), int(offsets[e + 1])
+        a3[e, :r1 - r0] = aq[r0:r1]
+        s3[e, :r1 - r0] = as_[r0:r1]
+    return a3, s3
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", GROUPED)
+def test_grouped_masked_layout(name):
+    # every expert owns max_m rows of which counts[e] are valid: the valid rows
+    # equal the contiguous layout's bit for bit (same configuration, same rows
+    # counted from the segment start) and the oracle; rows past a count keep
+    # their contents
+    device()
+    counts = [5, 0, 64, 1, 37, 64, 20, 0]
+    max_m, n, k = 64, 392, 768
+    aq, as_, bq, bs, offsets = _experts(counts, n, k, seed=17)
+    a3, s3 = _masked_inputs(counts, max_m, aq, as_, offsets)
+    m = int(offsets[-1])
+    cfg = _cfg(name)
+    B, BS = to_dev(bq), to_dev(bs)
+    for out in ("bf16", "fp32"):
+        flat = _grouped(to_dev(aq), to_dev(as_), B, BS, to_dev(offsets), m, n, k, out, cfg)
+        c3 = torch.full((len(counts), max_m, n), float("nan"), dtype=TORCH_OUT[out],
+                        device="cuda:0")
+        st = inferop_amd.w8a8_block_fp8_grouped_gemm_masked_config(
+            c3, to_dev(a3), to_dev(s3), B, BS, to_dev(np.array(counts, np.int32)), max_m, n, k,
+            len(counts), getattr(DT, out), cfg)
+        assert st == 0
+        for e, cnt in enumerate(counts):
+            r0 = int(offsets[e])
+            assert torch.equal(c3[e, :cnt], flat[r0:r0 + cnt]), f"{name} {out} expert {e}"
+            assert torch.isnan(c3[e, cnt:].float()).all(), f"{name} {out} expert {e} tail"
+            if cnt:
+                assert_gemm_close(out_to_f32(c3[e, :cnt]),
+                                  oracle.gemm(aq[r0:r0 + cnt], as_[r0:r0 + cnt], bq[e], bs[e]),
+                                  f"{name} {out} expert {e}")
+
+
+@pytest.mark.gpu
+def test_grouped_masked_counts_clamped_and_hint():
+    # counts are device data: negative counts act as 0 and counts past max_m
+    # as max_m; expected_m only steers the tile choice (the result is the same
+    # within the tolerance whatever the hint)
+    device()
+    counts = [-3, 40, 1000, 7]
+    eff = [0, 32, 32, 7]
+    max_m, n, k = 32, 256, 512
+    aq, as_, bq, bs, offsets = _experts(eff, n, k, seed=29)
+    a3, s3 = _masked_inputs(eff, max_m, aq, as_, offsets)
+    args = [to_dev(v) for v in (a3, s3, bq, bs, np.array(counts, np.int32))]
+    for hint in (0, 2, 20, 500):
+        c3 = torch.full((len(counts), max_m, n), float("nan"), device="cuda:0")
+        assert inferop_amd.w8a8_block_fp8_grouped_gemm_masked(
+            c3, *args, max_m, n, k, len(counts), hint, out_dt=DT.fp32) == 0
+        got = out_to_f32(c3)
+        assert np.isnan(got[0]).all()
+        for e in (1, 2, 3):
+            r0, cnt = int(offsets[e]), eff[e]
+            assert_gemm_close(got[e, :cnt], oracle.gemm(aq[r0:r0 + cnt], as_[r0:r0 + cnt], bq[e],
+                                                         bs[e]), f"hint {hint} expert {e}")
+            assert np.isnan(got[e, cnt:]).all()

@@ -216,6 +216,14 @@ def test_grouped_gemm_host_checks():
                         "pre_n128_m16_w8_s4"):
             assert gc(0, 0, 0, 0, 0, 0, 16, 512, 1024, 8, inferop_amd.dtype.bf16, i) == \
                 S.ERR_ARGUMENT, name
+    gm = inferop_amd.w8a8_block_fp8_grouped_gemm_masked
+    assert gm(0, 0, 0, 0, 0, 0, 8, 512, 1000, 8) == S.ERR_SHAPE
+    assert gm(0, 0, 0, 0, 0, 0, -1, 512, 1024, 8) == S.ERR_SHAPE
+    assert gm(0, 0, 0, 0, 0, 0, 1 << 20, 512, 1024, 1 << 12) == S.ERR_SHAPE  # rows past 2^31
+    assert gm(0, 0, 0, 0, 0, 0, 0, 512, 1024, 8) == S.OK
+    gmc = inferop_amd.w8a8_block_fp8_grouped_gemm_masked_config
+    assert gmc(0, 0, 0, 0, 0, 0, 8, 512, 1024, 8, inferop_amd.dtype.bf16,
+               names.index("pre_n256_m256_w8_s2")) == S.ERR_ARGUMENT
     sel = lambda m, e: names[inferop_amd.grouped_gemm_select(m, 4096, 7168, e)]
     assert sel(64 * 8, 256) == "pre_n128_m16_w8_s4"
     assert sel(20 * 256, 256) == "pre_n128_m32_w8_s4"
