@@ -1339,7 +1339,7 @@ const CfgEntry kCfgs[] = {
     PREFILL_GROUPED_CFG(128, 32, 8, 1, 4, "pre_n128_m32_w8_s4"),
     PREFILL_GROUPED_CFG(128, 16, 8, 1, 4, "pre_n128_m16_w8_s4"),
     PREFILL_CFG(64, 64, 4, 1, 4, "pre_n64_m64_w4_s4"),
-    PREFILL_CFG(128, 64, 8, 1, 3, "pre_n128_m64_w8_s3"),
+    PREFILL_GROUPED_CFG(128, 64, 8, 1, 3, "pre_n128_m64_w8_s3"),
     DECODE_LDS_CFG(2, 4, "decl_k2_u4"),
     DECODE_LDS_CFG(4, 4, "decl_k4_u4"),
     DECODE_LDS_CFG(8, 4, "decl_k8_u4"),

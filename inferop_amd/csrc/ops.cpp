@@ -330,17 +330,19 @@ int gemm_impl(void* c, const void* a_q, const void* a_scales, const void* b_q,
   return gemm_launch(c, a_q, a_scales, b_q, b_scales, m, n, k, out_dt, ch.cfg, ch.split, stream);
 }
 
-// Grouped (MoE expert) GEMM, contiguous layout.  One M tile height for all
-// experts, from the mean rows per expert: while experts get a few rows the
-// call streams every expert's weights once (HBM-bound) and 16-row tiles keep
-// the MFMA and LDS work near what the rows need; from about 24 rows per
-// expert the 128x128 tiles, which read each weight slice once per 128 rows,
-// win (measured at 32 experts, N=4096, K=7168: 8 rows per expert 193 us on
-// 16-row tiles vs 232 us on 128x128; 32 rows 303 us on 32-row tiles vs 248).
+// Grouped (MoE expert) GEMM.  One M tile height for all experts, from the
+// mean rows per expert: while experts get a few rows the call streams every
+// expert's weights once (HBM-bound) and short tiles keep the MFMA and LDS
+// work near what the rows need; with more rows the taller tiles read each
+// weight slice once per tile height.  Measured at 32 experts, N=4096,
+// K=7168: 8 rows per expert 193 us on 16-row tiles (232 us on 128x128);
+// 32 rows 216 us on 64-row three-stage tiles (245 us on 128x128, 303 us on
+// 32-row tiles); 128 rows 374 us on 128x128 (418 us on 64-row tiles).
 int32_t select_grouped(int64_t m, int64_t num_experts) {
   const int64_t avg = m / (num_experts > 0 ? num_experts : 1);
   if (avg < 16) return kPreN128M16S4;
   if (avg < 24) return kPreN128M32S4;
+  if (avg < 64) return kPreN128M64S3;
   return kPreN128M128S2;
 }
 

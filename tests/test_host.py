@@ -213,7 +213,7 @@ def test_grouped_gemm_host_checks():
     gc = inferop_amd.w8a8_block_fp8_grouped_gemm_config
     for i, name in enumerate(names):
         if name not in ("pre_n128_m128_w4_s2", "pre_n128_m64_w8_s4", "pre_n128_m32_w8_s4",
-                        "pre_n128_m16_w8_s4"):
+                        "pre_n128_m16_w8_s4", "pre_n128_m64_w8_s3"):
             assert gc(0, 0, 0, 0, 0, 0, 16, 512, 1024, 8, inferop_amd.dtype.bf16, i) == \
                 S.ERR_ARGUMENT, name
     gm = inferop_amd.w8a8_block_fp8_grouped_gemm_masked
@@ -227,7 +227,8 @@ def test_grouped_gemm_host_checks():
     sel = lambda m, e: names[inferop_amd.grouped_gemm_select(m, 4096, 7168, e)]
     assert sel(64 * 8, 256) == "pre_n128_m16_w8_s4"
     assert sel(20 * 256, 256) == "pre_n128_m32_w8_s4"
-    assert sel(32 * 256, 256) == "pre_n128_m128_w4_s2"
+    assert sel(32 * 256, 256) == "pre_n128_m64_w8_s3"
+    assert sel(64 * 256, 256) == "pre_n128_m128_w4_s2"
     assert sel(4096 * 8, 256) == "pre_n128_m128_w4_s2"
 
 
