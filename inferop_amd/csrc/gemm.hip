@@ -733,6 +733,33 @@ __device__ __forceinline__ bool grouped_tile(const GemmArgs& a, int tmv, int lan
   return false;
 }
 
+// Number of (expert, row block) M tiles: the sum of ceil(rows / BM) over the
+// experts, rows as grouped_tile forms them.
+template <int BM>
+__device__ __forceinline__ int grouped_mtiles(const GemmArgs& a, int lane) {
+  const int M = a.m, E = a.experts;
+  int total = 0;
+  for (int c0 = 0; c0 < E; c0 += 64) {
+    const int ei = c0 + lane;
+    int cnt = 0;
+    if (ei < E) {
+      int lo, hi;
+      if (a.max_m > 0) {
+        lo = ei * a.max_m;
+        hi = lo + min(max(a.offsets[ei], 0), a.max_m);
+      } else {
+        lo = min(max(a.offsets[ei], 0), M);
+        hi = min(max(a.offsets[ei + 1], lo), M);
+      }
+      cnt = (hi - lo + BM - 1) / BM;
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) cnt += __shfl_xor(cnt, d);
+    total += cnt;
+  }
+  return __builtin_amdgcn_readfirstlane(total);
+}
+
 template <int BN, int BM, int WN, int WM, int STAGES, int OUT_DT, bool GROUPED = false>
 __global__ __launch_bounds__(64 * WN * WM) void gemm_prefill_kernel(GemmArgs a) {
   constexpr int NW = WN * WM;
@@ -1009,7 +1036,7 @@ __host__ __device__ constexpr int pass_rows(int bm, int fit) {
   return (bm <= fit || bm <= 16) ? bm : pass_rows(bm / 2, fit);
 }
 
-template <int BN, int BM, int WN, int WM, int OUT_DT>
+template <int BN, int BM, int WN, int WM, int OUT_DT, bool GROUPED = false>
 __global__ __launch_bounds__(64 * WN * WM) void gemm_persist_kernel(GemmArgs a) {
   using OT = typename OutT<OUT_DT>::T;
   constexpr int NW = WN * WM;
@@ -1050,10 +1077,25 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_persist_kernel(GemmArgs a) 
   const int KG = K >> 7;
   const int NB = (N + 127) >> 7;
   const int tiles_n = (N + BN - 1) / BN, tiles_m = (M + BM - 1) / BM;
-  const int tiles = tiles_n * tiles_m;
+  // grouped: the experts' M tiles, each with every N tile (N tile fastest)
+  const int tiles = tiles_n * (GROUPED ? grouped_mtiles<BM>(a, lane) : tiles_m);
   const int P = gridDim.x;
   int u = xcd_contiguous((int)blockIdx.x, P);
   if (u >= tiles) return;
+  // tile uu: first column n0, rows [m0, mend), expert e (0 when not grouped)
+  auto tile_at = [&](int uu, int* n0, int* m0, int* mend, int* e) {
+    if constexpr (GROUPED) {
+      (void)grouped_tile<BM>(a, uu / tiles_n, lane, e, m0, mend);
+      *n0 = (uu % tiles_n) * BN;
+    } else {
+      int tn, tm;
+      tile_of(uu, tiles_n, tiles_m, &tn, &tm);
+      *n0 = tn * BN;
+      *m0 = tm * BM;
+      *mend = M;
+      *e = 0;
+    }
+  };
 
   const int lrow = lane >> 3;
   const int loff = lrow * K + ((lane & 7) ^ lrow) * 16;
@@ -1117,15 +1159,15 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_persist_kernel(GemmArgs a) 
     const float* sa_src = a.as;
     const float* sb_src = a.bs;
     // tile buffers: rows past the last row of A or B read as zeros
-    auto set_loads = [&](int n0, int m0) {
+    auto set_loads = [&](int n0, int m0, int mend, int e) {
       if constexpr (kLoader) {
-        const int nrows = min(BN, N - n0), mrows = min(BM, M - m0);
-        rB = rsrc_words(a.bq + (int64_t)n0 * K, (uint32_t)(nrows * K));
+        const int nrows = min(BN, N - n0), mrows = min(BM, mend - m0);
+        rB = rsrc_words(a.bq + ((int64_t)e * N + n0) * K, (uint32_t)(nrows * K));
         rA = rsrc_words(a.aq + (int64_t)m0 * K, (uint32_t)(mrows * K));
-        sa_src = a.as + (int64_t)(m0 + min(min(l, kSaBlocks - 1) * 64 + lane, M - 1 - m0)) * KG;
+        sa_src = a.as + (int64_t)(m0 + min(min(l, kSaBlocks - 1) * 64 + lane, mend - 1 - m0)) * KG;
         constexpr int kSbBlocks = BN >= 128 ? BN / 128 : 1;
         const int nb = min((n0 >> 7) + min(lane, kSbBlocks - 1), NB - 1);
-        sb_src = a.bs + (int64_t)nb * KG;
+        sb_src = a.bs + ((int64_t)e * NB + nb) * KG;
       }
     };
     // Load d of a stage: 0 the activation scales, 1 the weight scales, then
@@ -1159,23 +1201,17 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_persist_kernel(GemmArgs a) 
       };
     };
 
-    int tn, tm;
-    tile_of(u, tiles_n, tiles_m, &tn, &tm);
-    int n0 = tn * BN, m0 = tm * BM;
-    set_loads(n0, m0);
+    int n0, m0, mend, ex;
+    tile_at(u, &n0, &m0, &mend, &ex);
+    set_loads(n0, m0, mend, ex);
 #pragma unroll
     for (int d = 0; d < kLoads; ++d) issue_load(0, smem0, d);
     barrier();
     for (;;) {
       const int nu = u + P;
       const bool has_next = nu < tiles;
-      int nn0 = n0, nm0 = m0;
-      if (has_next) {
-        int ntn, ntm;
-        tile_of(nu, tiles_n, tiles_m, &ntn, &ntm);
-        nn0 = ntn * BN;
-        nm0 = ntm * BM;
-      }
+      int nn0 = n0, nm0 = m0, nmend = mend, nex = ex;
+      if (has_next) tile_at(nu, &nn0, &nm0, &nmend, &nex);
 #pragma unroll
       for (int i = 0; i < SN; ++i)
 #pragma unroll
@@ -1194,7 +1230,7 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_persist_kernel(GemmArgs a) 
       barrier();  // group KG - 1 landed; every wave is done with buffer 0
       // the next tile's first group (the last tile reloads its own, which
       // keeps the group free of branches)
-      set_loads(nn0, nm0);
+      set_loads(nn0, nm0, nmend, nex);
       compute(smem1, spread(0, smem0));
       pin_acc();
       barrier();  // the next tile's group 0 landed; buffer 1 is free
@@ -1239,7 +1275,7 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_persist_kernel(GemmArgs a) 
             for (int q = 0; q < QB; ++q) {
               const int idx = (wave - NL) * 64 + lane + (q0 + q) * 64 * NS;
               const int m = m0 + p * RP + idx / kChunks, n = n0 + (idx % kChunks) * (16 / kOB);
-              if (m >= M || n >= N) continue;
+              if (m >= mend || n >= N) continue;
               OT* dst = C + (int64_t)m * N + n;
               if (vec && n + 16 / kOB - 1 < N) {
                 __builtin_nontemporal_store(piece[q], reinterpret_cast<u32x4*>(dst));
@@ -1256,6 +1292,8 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_persist_kernel(GemmArgs a) 
       u = nu;
       n0 = nn0;
       m0 = nm0;
+      mend = nmend;
+      ex = nex;
     }
   };
   if (wave < NL) {
@@ -1274,9 +1312,9 @@ struct CfgEntry {
   int bn, bm, waves;
   const char* name;
   KernelFn fn[3];  // [out_dt index]
-  // tiled (kind 2): the grouped-expert variant, where built (else null);
-  // wide decode (kind 4): the variant without the scale preload, for more
-  // than wide_scale_cap(MT) groups per wave
+  // tiled (kind 2) and persistent (kind 3): the grouped-expert variant, where
+  // built (else null); wide decode (kind 4): the variant without the scale
+  // preload, for more than wide_scale_cap(MT) groups per wave
   KernelFn fn_alt[3];
 };
 
@@ -1319,9 +1357,16 @@ struct CfgEntry {
     gemm_decode_wide_kernel<MT, WK, UW, UA, false, kFp16>,                                     \
     gemm_decode_wide_kernel<MT, WK, UW, UA, false, kBf16>}}
 #define PERSIST_CFG(BN, BM, WN, WM, NAME)                                                      \
-  {3, BN, BM, WN * WM, NAME,                                                                   \
+  {3,                                                                                          \
+   BN,                                                                                         \
+   BM,                                                                                         \
+   WN * WM,                                                                                    \
+   NAME,                                                                                       \
    {gemm_persist_kernel<BN, BM, WN, WM, kFp32>, gemm_persist_kernel<BN, BM, WN, WM, kFp16>,     \
-    gemm_persist_kernel<BN, BM, WN, WM, kBf16>}}
+    gemm_persist_kernel<BN, BM, WN, WM, kBf16>},                                               \
+   {gemm_persist_kernel<BN, BM, WN, WM, kFp32, true>,                                          \
+    gemm_persist_kernel<BN, BM, WN, WM, kFp16, true>,                                          \
+    gemm_persist_kernel<BN, BM, WN, WM, kBf16, true>}}
 
 const CfgEntry kCfgs[] = {
     DECODE_CFG(1, 1, 8, "dec_m16_k1_u8"),
@@ -1458,7 +1503,7 @@ extern "C" int inferop_hip_gemm_config_info(int32_t cfg, inferop_gemm_cfg_info* 
   info->waves = kCfgs[cfg].waves;
   info->kind = kCfgs[cfg].kind;
   info->name = kCfgs[cfg].name;
-  info->grouped = kCfgs[cfg].kind == 2 && kCfgs[cfg].fn_alt[0] != nullptr;
+  info->grouped = (kCfgs[cfg].kind == 2 || kCfgs[cfg].kind == 3) && kCfgs[cfg].fn_alt[0] != nullptr;
   return hipSuccess;
 }
 
@@ -1542,7 +1587,8 @@ extern "C" int inferop_hip_gemm_w8a8_block_grouped(void* c, const uint8_t* a_q,
   const int di = dt_index(out_dt);
   if (di < 0 || cfg < 0 || cfg >= kNumCfgs) return hipErrorInvalidValue;
   const CfgEntry& cf = kCfgs[cfg];
-  if (cf.kind != 2 || !cf.fn_alt[di]) return hipErrorInvalidValue;
+  if ((cf.kind != 2 && cf.kind != 3) || !cf.fn_alt[di]) return hipErrorInvalidValue;
+  if (cf.kind == 3 && (k / 128) % 2 != 0) return hipErrorInvalidValue;
   if (m < 0 || n <= 0 || k <= 0 || k % 128 != 0 || experts <= 0 || max_m < 0)
     return hipErrorInvalidValue;
   // masked layout: m is the experts' max_m-row blocks end to end
@@ -1562,7 +1608,16 @@ extern "C" int inferop_hip_gemm_w8a8_block_grouped(void* c, const uint8_t* a_q,
   GemmArgs args{c,      a_q,    a_scales,     b_q,         b_scales,
                 nullptr, nullptr, (int)m,     (int)n,      (int)k,
                 vec_ok, offsets, (int)experts, (int)max_m};
-  hipLaunchKernelGGL(cf.fn_alt[di], dim3((unsigned)(tn * tmv), 1u), dim3(64 * cf.waves), 0, st,
-                     args);
+  int64_t grid = tn * tmv;
+  if (cf.kind == 3) {
+    // persistent: one workgroup per CU (two for 128x128 tiles) walks the
+    // tiles, whose number the kernel takes from the offsets
+    int cus = 0;
+    hipError_t e = device_cus(&cus);
+    if (e != hipSuccess) return e;
+    const int64_t slots = (int64_t)cus * (cf.bn * cf.bm <= 128 * 128 ? 2 : 1);
+    if (grid > slots) grid = slots;
+  }
+  hipLaunchKernelGGL(cf.fn_alt[di], dim3((unsigned)grid, 1u), dim3(64 * cf.waves), 0, st, args);
   return hipGetLastError();
 }

@@ -330,16 +330,19 @@ int gemm_impl(void* c, const void* a_q, const void* a_scales, const void* b_q,
   return gemm_launch(c, a_q, a_scales, b_q, b_scales, m, n, k, out_dt, ch.cfg, ch.split, stream);
 }
 
-// Grouped (MoE expert) GEMM.  One M tile height for all experts, from the
-// mean rows per expert: while experts get a few rows the call streams every
-// expert's weights once (HBM-bound) and short tiles keep the MFMA and LDS
-// work near what the rows need; with more rows the taller tiles read each
-// weight slice once per tile height.  Measured at 32 experts, N=4096,
-// K=7168: 8 rows per expert 193 us on 16-row tiles (232 us on 128x128);
-// 32 rows 216 us on 64-row three-stage tiles (245 us on 128x128, 303 us on
-// 32-row tiles); 128 rows 374 us on 128x128 (418 us on 64-row tiles).
-int32_t select_grouped(int64_t m, int64_t num_experts) {
+// Grouped (MoE expert) GEMM: the configuration from the mean rows per expert.
+// With an even K / 128 the persistent kernels, whose load pipeline runs on
+// across a workgroup's tiles, stream the experts' weights best whatever the
+// rows: two 128x128 workgroups per CU below about 96 rows per expert, one
+// 256x256 beyond (measured at 32 experts, N=4096, K=7168: 2 rows per expert
+// 153 us on 128x128 vs 155 us on 16-row tiled; 32 rows 178 vs 217 us; 64 rows
+// 191 us vs 239 us on 256x256; 128 rows 251 us on 256x256 vs 286 us on
+// 128x128 and 385 us tiled; 512 rows 592 vs 843 us tiled).  With an odd
+// K / 128 the tiled kernels: 16-row tiles below 16 rows per expert, 32-row
+// below 24, 64-row three-stage below 64, 128x128 beyond.
+int32_t select_grouped(int64_t m, int64_t k, int64_t num_experts) {
   const int64_t avg = m / (num_experts > 0 ? num_experts : 1);
+  if ((k / 128) % 2 == 0) return avg < 96 ? kPerN128M128 : kPerN256M256;
   if (avg < 16) return kPreN128M16S4;
   if (avg < 24) return kPreN128M32S4;
   if (avg < 64) return kPreN128M64S3;
@@ -393,7 +396,7 @@ int masked_impl(void* c, const void* a_q, const void* a_scales, const void* b_q,
   if (!valid_input_dtype(out_dt)) return INFEROP_ERR_DTYPE;
   if (cfg < 0) {
     const int64_t rows = expected_m > 0 ? (expected_m < max_m ? expected_m : max_m) : max_m;
-    cfg = select_grouped(rows * experts, experts);
+    cfg = select_grouped(rows * experts, k, experts);
   }
   if (max_m == 0) return INFEROP_OK;
   if (!gemm_device()) return INFEROP_ERR_DEVICE;
@@ -410,7 +413,7 @@ int grouped_impl(void* c, const void* a_q, const void* a_scales, const void* b_q
   if (m == 0) return INFEROP_OK;
   if (!gemm_device()) return INFEROP_ERR_DEVICE;
   return grouped_launch(c, a_q, a_scales, b_q, b_scales, offsets, m, n, k, experts, 0, out_dt,
-                        select_grouped(m, experts), stream);
+                        select_grouped(m, k, experts), stream);
 }
 
 }  // namespace
@@ -605,6 +608,7 @@ extern "C" int inferop_w8a8_block_fp8_grouped_gemm_config(
   if (config < 0 || config >= inferop_hip_gemm_num_configs() ||
       inferop_hip_gemm_config_info(config, &info) != 0 || !info.grouped)
     return INFEROP_ERR_ARGUMENT;
+  if (info.kind == 3 && (k / 128) % 2 != 0) return INFEROP_ERR_ARGUMENT;
   if (m == 0) return INFEROP_OK;
   if (!gemm_device()) return INFEROP_ERR_DEVICE;
   return grouped_launch(c, a_q, a_scales, b_q, b_scales, expert_offsets, m, n, k, num_experts, 0,
@@ -627,6 +631,7 @@ extern "C" int inferop_w8a8_block_fp8_grouped_gemm_masked_config(
   if (config < 0 || config >= inferop_hip_gemm_num_configs() ||
       inferop_hip_gemm_config_info(config, &info) != 0 || !info.grouped)
     return INFEROP_ERR_ARGUMENT;
+  if (info.kind == 3 && (k / 128) % 2 != 0) return INFEROP_ERR_ARGUMENT;
   return masked_impl(c, a_q, a_scales, b_q, b_scales, masked_m, max_m, n, k, num_experts, 0, 128,
                      128, out_dt, config, stream);
 }
@@ -635,7 +640,7 @@ extern "C" int inferop_grouped_gemm_select(int64_t m, int64_t n, int64_t k, int6
                                            int32_t* config) {
   if (m < 0 || n <= 0 || k <= 0 || k % 128 != 0 || num_experts <= 0 || !config)
     return INFEROP_ERR_ARGUMENT;
-  *config = select_grouped(m, num_experts);
+  *config = select_grouped(m, k, num_experts);
   return INFEROP_OK;
 }
 

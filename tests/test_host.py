@@ -213,7 +213,8 @@ def test_grouped_gemm_host_checks():
     gc = inferop_amd.w8a8_block_fp8_grouped_gemm_config
     for i, name in enumerate(names):
         if name not in ("pre_n128_m128_w4_s2", "pre_n128_m64_w8_s4", "pre_n128_m32_w8_s4",
-                        "pre_n128_m16_w8_s4", "pre_n128_m64_w8_s3"):
+                        "pre_n128_m16_w8_s4", "pre_n128_m64_w8_s3", "per_n256_m256_w8",
+                        "per_n256_m128_w8", "per_n128_m128_w4"):
             assert gc(0, 0, 0, 0, 0, 0, 16, 512, 1024, 8, inferop_amd.dtype.bf16, i) == \
                 S.ERR_ARGUMENT, name
     gm = inferop_amd.w8a8_block_fp8_grouped_gemm_masked
@@ -224,7 +225,15 @@ def test_grouped_gemm_host_checks():
     gmc = inferop_amd.w8a8_block_fp8_grouped_gemm_masked_config
     assert gmc(0, 0, 0, 0, 0, 0, 8, 512, 1024, 8, inferop_amd.dtype.bf16,
                names.index("pre_n256_m256_w8_s2")) == S.ERR_ARGUMENT
+    # the persistent grouped kernels take an even K / 128
+    assert gc(0, 0, 0, 0, 0, 0, 16, 512, 1152, 8, inferop_amd.dtype.bf16,
+              names.index("per_n256_m256_w8")) == S.ERR_ARGUMENT
+    # even K / 128: the persistent kernels; odd: the tiled ones
     sel = lambda m, e: names[inferop_amd.grouped_gemm_select(m, 4096, 7168, e)]
+    assert sel(64 * 8, 256) == "per_n128_m128_w4"
+    assert sel(64 * 256, 256) == "per_n128_m128_w4"
+    assert sel(128 * 256, 256) == "per_n256_m256_w8"
+    sel = lambda m, e: names[inferop_amd.grouped_gemm_select(m, 4096, 7168 + 128, e)]
     assert sel(64 * 8, 256) == "pre_n128_m16_w8_s4"
     assert sel(20 * 256, 256) == "pre_n128_m32_w8_s4"
     assert sel(32 * 256, 256) == "pre_n128_m64_w8_s3"
