@@ -54,3 +54,51 @@ def test_graph_replays_match_eager(m, n, k):
         with torch.cuda.stream(st):
             run()
         st.synchronize()
+
+
+@pytest.mark.gpu
+def test_graph_grouped_masked_routing_changes_between_replays():
+    # the masked grouped GEMM is what a captured MoE decode step calls: the
+    # shapes are fixed and only the per-expert counts on the device change.
+    # Capture once, write new counts before each replay, and every replay must
+    # equal an eager call with those counts (valid rows) and leave the other
+    # rows alone.
+    device()
+    experts, max_m, n, k = 8, 16, 384, 1024
+    g_ = np.random.default_rng(4)
+    a = bf16_dev(datagen.f32_to_bf16_bits(
+        g_.standard_normal((experts * max_m, k)).astype(np.float32)))
+    aq, as_ = inferop_amd.quantize(a)
+    bq, bs = zip(*[oracle.weight_block_quant(datagen.weights(n, k, 90 + e))
+                   for e in range(experts)])
+    bqd, bsd = to_dev(np.stack(bq)), to_dev(np.stack(bs))
+    counts = torch.zeros(experts, dtype=torch.int32, device="cuda:0")
+    c = torch.empty((experts, max_m, n), dtype=torch.float32, device="cuda:0")
+    st = torch.cuda.Stream()
+
+    def run(out):
+        assert inferop_amd.w8a8_block_fp8_grouped_gemm_masked(
+            out, aq, as_, bqd, bsd, counts, max_m, n, k, experts, 4, out_dt=DT.fp32,
+            stream=st.cuda_stream) == 0
+
+    counts.copy_(torch.full((experts,), max_m, dtype=torch.int32))
+    with torch.cuda.stream(st):
+        run(c)  # eager first: nothing to allocate inside the capture
+    st.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        run(c)
+    for rep in range(4):
+        cnt = g_.integers(0, max_m + 1, experts).astype(np.int32)
+        counts.copy_(torch.from_numpy(cnt))
+        c.fill_(-7.0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        want = torch.full_like(c, -7.0)
+        with torch.cuda.stream(st):
+            run(want)
+        st.synchronize()
+        assert torch.equal(c, want), f"replay {rep}"
+        for e in range(experts):
+            assert (c[e, cnt[e]:] == -7.0).all(), f"replay {rep} expert {e}"
