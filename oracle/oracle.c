@@ -186,12 +186,12 @@ void orc_dequant_fp8_per_token_group(float* x, const uint8_t* q, const float* sc
       x[r * cols + c] = orc_e4m3_to_float(q[r * cols + c]) * scales[r * gpr + c / group_size];
 }
 
-/* reference.cpp:99-108 for one output row. */
-static void gemm_row(float* crow, int64_t mi, const uint8_t* a_q, const float* a_scales,
-                     const uint8_t* b_q, const float* b_scales, int64_t n, int64_t k,
-                     int32_t group_size, int32_t block_n) {
+/* reference.cpp:99-108 for output row mi, columns [n0, n1). */
+static void gemm_cols(float* crow, int64_t mi, const uint8_t* a_q, const float* a_scales,
+                      const uint8_t* b_q, const float* b_scales, int64_t n0, int64_t n1,
+                      int64_t k, int32_t group_size, int32_t block_n) {
   const int64_t kg = k / group_size;
-  for (int64_t ni = 0; ni < n; ++ni) {
+  for (int64_t ni = n0; ni < n1; ++ni) {
     double acc = 0.0;
     for (int64_t ki = 0; ki < k; ++ki) {
       float sa = a_scales[mi * kg + ki / group_size];
@@ -204,15 +204,24 @@ static void gemm_row(float* crow, int64_t mi, const uint8_t* a_q, const float* a
   }
 }
 
+/* Work items are (output row, 64-column block): every element still sums its
+ * k products in the reference's order, so any thread count gives the same
+ * bits; the column blocks let one-row products use every thread. */
+#define ORC_COLS 64
+
 void orc_w8a8_block_fp8_gemm(float* c, const uint8_t* a_q, const float* a_scales,
                              const uint8_t* b_q, const float* b_scales, int64_t m, int64_t n,
                              int64_t k, int32_t group_size, int32_t block_n, int32_t threads) {
+  const int64_t nc = (n + ORC_COLS - 1) / ORC_COLS;
 #ifdef _OPENMP
   if (threads <= 0) threads = omp_get_max_threads();
 #pragma omp parallel for schedule(dynamic, 1) num_threads(threads)
 #endif
-  for (int64_t mi = 0; mi < m; ++mi)
-    gemm_row(c + mi * n, mi, a_q, a_scales, b_q, b_scales, n, k, group_size, block_n);
+  for (int64_t w = 0; w < m * nc; ++w) {
+    const int64_t mi = w / nc, n0 = (w % nc) * ORC_COLS;
+    gemm_cols(c + mi * n, mi, a_q, a_scales, b_q, b_scales, n0,
+              n0 + ORC_COLS < n ? n0 + ORC_COLS : n, k, group_size, block_n);
+  }
   (void)threads;
 }
 
@@ -221,12 +230,16 @@ void orc_w8a8_block_fp8_gemm_rows(float* c, const uint8_t* a_q, const float* a_s
                                   int64_t k, int32_t group_size, int32_t block_n,
                                   const int64_t* rows, int64_t nrows, int32_t threads) {
   (void)m;
+  const int64_t nc = (n + ORC_COLS - 1) / ORC_COLS;
 #ifdef _OPENMP
   if (threads <= 0) threads = omp_get_max_threads();
 #pragma omp parallel for schedule(dynamic, 1) num_threads(threads)
 #endif
-  for (int64_t i = 0; i < nrows; ++i)
-    gemm_row(c + i * n, rows[i], a_q, a_scales, b_q, b_scales, n, k, group_size, block_n);
+  for (int64_t w = 0; w < nrows * nc; ++w) {
+    const int64_t i = w / nc, n0 = (w % nc) * ORC_COLS;
+    gemm_cols(c + i * n, rows[i], a_q, a_scales, b_q, b_scales, n0,
+              n0 + ORC_COLS < n ? n0 + ORC_COLS : n, k, group_size, block_n);
+  }
   (void)threads;
 }
 

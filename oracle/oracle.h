@@ -35,8 +35,9 @@ void orc_quant_fp8_per_token_group(uint8_t* q, float* scales, const float* x, in
 /* reference/reference.cpp:82-91 */
 void orc_dequant_fp8_per_token_group(float* x, const uint8_t* q, const float* scales,
                                      int64_t rows, int64_t cols, int32_t group_size);
-/* reference/reference.cpp:93-110, whole output, rows spread over OpenMP threads
- * (per-element arithmetic and summation order unchanged). */
+/* reference/reference.cpp:93-110, whole output; (row, 64-column block) items
+ * spread over OpenMP threads (per-element arithmetic and summation order
+ * unchanged, so the result does not depend on the thread count). */
 void orc_w8a8_block_fp8_gemm(float* c, const uint8_t* a_q, const float* a_scales,
                              const uint8_t* b_q, const float* b_scales, int64_t m, int64_t n,
                              int64_t k, int32_t group_size, int32_t block_n, int32_t threads);

@@ -185,6 +185,20 @@ def test_gemm_bit_exact_vs_reference():
     assert np.array_equal(oracle.gemm_rows(aq, as_, bq, bs, rows), c[rows])
 
 
+def test_gemm_thread_count_does_not_change_bits():
+    # the oracle splits the output into (row, 64-column block) items across
+    # threads; each element keeps the reference's summation order
+    a_bits, a_f32, bq, bs = datagen.gemm_case(3, 200, 256, seed=8)
+    aq, as_ = oracle.quant(a_f32)
+    one = oracle.gemm(aq, as_, bq, bs, threads=1)
+    assert np.array_equal(one.view(np.uint32), oracle.ref_gemm(aq, as_, bq, bs).view(np.uint32))
+    for t in (2, 5, 8):
+        assert np.array_equal(oracle.gemm(aq, as_, bq, bs, threads=t).view(np.uint32),
+                              one.view(np.uint32))
+    rows = np.array([2, 0])
+    assert np.array_equal(oracle.gemm_rows(aq, as_, bq, bs, rows, threads=3), one[rows])
+
+
 def test_gemm_vs_float64_matmul_of_dequantized_operands():
     a_bits, a_f32, bq, bs = datagen.gemm_case(20, 260, 384, seed=4)
     aq, as_ = oracle.quant(a_f32)
