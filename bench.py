@@ -252,6 +252,7 @@ def main():
                          "avg_launch_us": round(g_ms / len(cases) * 1e3, 3)},
             "decode_detail": detail,
             "quant_decode_gbs": round(q_bytes / (q_ms * 1e-3) / 1e9, 1),
+            "gpu_clocks": gpu_clocks(),
         })
         del step_graphs, W, A, AQ, C
         torch.cuda.empty_cache()
@@ -483,6 +484,24 @@ def main():
     if not args.no_cpu:
         result["cpu_baseline"], result["cpu_baseline_parallel"] = cpu_baseline()
     print(json.dumps(result), flush=True)
+
+
+def gpu_clocks():
+    """The clock lines `rocm-smi --showclocks` prints right after the decode
+    timing (a child process with its own time limit), or None where the tool
+    is missing or fails: context for the measured rates, not a measurement."""
+    import shutil
+    import subprocess
+    exe = shutil.which("rocm-smi")
+    if exe is None:
+        return None
+    try:
+        out = subprocess.run([exe, "--showclocks"], capture_output=True, text=True,
+                             timeout=20).stdout
+    except (OSError, subprocess.SubprocessError):
+        return None
+    lines = [ln.strip() for ln in out.splitlines() if "clk" in ln.lower() and ":" in ln]
+    return lines or None
 
 
 def cpu_baseline():
