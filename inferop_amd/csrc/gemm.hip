@@ -1108,23 +1108,26 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_persist_kernel(GemmArgs a) 
     const uint8_t* bB = st;
     const uint8_t* bA = st + kOffA;
     const float* sA = reinterpret_cast<const float*>(st + kOffSA);
-    const float sbC = reinterpret_cast<const float*>(st + kOffSB)[(wn * TN) >> 7];
+    // Plain GEMM: the weight operand of slice i+1 is read while slice i is
+    // multiplied, so its LDS latency is not waited out before the slice's
+    // first MFMA (256x256 tiles: 7168x16384 470 -> 459 us, 24576x1536
+    // 167 -> 163 us), and the first slice's operands are read ahead of the
+    // scales, so the group's first MFMA does not wait for the scale reads
+    // (LDS returns in order; 7168x16384 471 -> 468 us).  The grouped forms
+    // keep the read in the slice: with the prefetch they lost time (32
+    // experts, N=4096, K=7168: 2 rows per expert on 128x128 tiles 152 -> 177
+    // us, 128 rows on 256x256 254 -> 261 us).
+    constexpr bool kPrefetch = !GROUPED;
+    i32x8 bnext{};
+    if constexpr (kPrefetch) bnext = lds_operand(bB, wn * TN + rsub, c0);
     i32x8 aop[SM];
 #pragma unroll
     for (int j = 0; j < SM; ++j) aop[j] = lds_operand(bA, wm * TM + 16 * j + rsub, c0);
+    const float sbC = reinterpret_cast<const float*>(st + kOffSB)[(wn * TN) >> 7];
     float sab[SM];
 #pragma unroll
     for (int j = 0; j < SM; ++j) sab[j] = sA[wm * TM + 16 * j + rsub] * sbC;
     constexpr int PJ = SM >= 4 ? 2 : SM;
-    // Plain GEMM: the weight operand of slice i+1 is read while slice i is
-    // multiplied, so its LDS latency is not waited out before the slice's
-    // first MFMA (256x256 tiles: 7168x16384 470 -> 459 us, 24576x1536
-    // 167 -> 163 us).  The grouped forms keep the read in the slice: with the
-    // prefetch they lost time (32 experts, N=4096, K=7168: 2 rows per expert
-    // on 128x128 tiles 152 -> 177 us, 128 rows on 256x256 254 -> 261 us).
-    constexpr bool kPrefetch = !GROUPED;
-    i32x8 bnext{};
-    if constexpr (kPrefetch) bnext = lds_operand(bB, wn * TN + rsub, c0);
 #pragma unroll
     for (int i = 0; i < SN; ++i) {
       i32x8 bop;
