@@ -15,11 +15,14 @@ bytes as a reference point), the quantizer, weight quantizer and fused
 producers on large inputs in GB/s, MoE routing, the grouped GEMM over MoE
 experts (decode- and prefill-sized routings), and a CPU baseline (the
 reference's own CPU golden code, or the oracle restatement, timed
-single-threaded on this host over the same decode workload).
+single-threaded on this host over the same decode workload, and the oracle's
+GEMM spread over the host cores beside it).
 Per-kernel durations come from HIP events on the launch stream around graph
 replays of back-to-back launches of one kernel.
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+       python bench.py --traffic-pass   (decode kernels once each, for FETCH_SIZE/WRITE_SIZE)
+       python bench.py --mfma-pass      (prefill GEMMs, for the MFMA and LDS counters)
 """
 from __future__ import annotations
 
@@ -69,6 +72,10 @@ def parse():
                    help="launch a 256 MiB streaming kernel and every decode-step kernel once "
                         "each (cold weights) for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs; "
                         "prints the launches in order with their algorithmic bytes")
+    p.add_argument("--mfma-pass", action="store_true",
+                   help="launch the GEMM of every prefill shape (M=4096) three times, "
+                        "synchronizing after each, for rocprofv3 --pmc runs of the MFMA "
+                        "counters; prints the launches in order with their flops")
     return p.parse_args()
 
 
@@ -113,10 +120,45 @@ def traffic_pass():
     print(json.dumps({"traffic_pass": launches}), flush=True)
 
 
+def mfma_pass():
+    """Counter-collection workload for the prefill GEMM: per configs[2] shape,
+    the activations are quantized on the GPU, then the GEMM runs three times
+    (bf16 out), each launch on its own, so per-dispatch counters (MFMA busy
+    cycles, active cycles) belong to one GEMM."""
+    import torch
+
+    import inferop_amd as ia
+
+    ia.lib()
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    launches = []
+    m = 4096
+    for (n, k) in PREFILL_NK:
+        v = torch.randint(0, 0x7E, (n, k), generator=gen, device=dev, dtype=torch.int32)
+        sgn = torch.randint(0, 2, (n, k), generator=gen, device=dev, dtype=torch.int32) << 7
+        bq = (v | sgn).to(torch.uint8)
+        bs = torch.rand(((n + 127) // 128, k // 128), generator=gen, device=dev) * 1e-3 + 1e-4
+        q, s = ia.quantize(torch.randn((m, k), generator=gen, device=dev).to(torch.bfloat16))
+        torch.cuda.synchronize()
+        launches.append({"launch": f"quant m={m} k={k}"})
+        cfg, split = ia.gemm_select(m, n, k)
+        for _ in range(3):
+            ia.gemm(q, s, bq, bs)
+            torch.cuda.synchronize()
+            launches.append({"launch": f"gemm m={m} n={n} k={k} {ia.gemm_config_name(cfg)}/s{split}",
+                             "flops": 2 * m * n * k})
+        del bq, bs, q, s
+    print(json.dumps({"mfma_pass": launches}), flush=True)
+
+
 def main():
     args = parse()
     if args.traffic_pass:
         traffic_pass()
+        return
+    if args.mfma_pass:
+        mfma_pass()
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this benchmark runs on exactly one GPU: the FP8 path has no "
