@@ -162,8 +162,8 @@ def main():
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this benchmark runs on exactly one GPU: the FP8 path has no "
-                                   "multi-GPU component here (sharding is described in "
-                                   "DESIGN.md); run with --gpus 1"}))
+                                   "multi-GPU component here (each GPU would run its own shard "
+                                   "of M, N or K with these kernels); run with --gpus 1"}))
         sys.exit(2)
     import numpy as np
     import torch
