@@ -64,6 +64,43 @@ def test_config1_decode_full_parity(m, nk):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("m,n,k,out,rtol,atol", [
+    (256, 256, 512, "fp32", 2e-3, 2e-2),
+    (256, 256, 512, "bf16", 1e-2, 3e-2),
+    (100, 180, 256, "fp32", 2e-3, 2e-2),
+    (4096, 4096, 4096, "bf16", 1e-2, 3e-2),
+])
+def test_reference_gpu_cross_check(m, n, k, out, rtol, atol):
+    """The reference's own GPU cross-check (tests/test_gemm.cpp:62-96) on its four
+    cases: A and W from N(0, 1) in fp32, A quantized per token group
+    (reference.cpp:65-80), W per 128x128 block with the reciprocal
+    (test_gemm.cpp:28-45), and every element within atol + rtol * |want| of the
+    CPU reference (test_util.h:44-63) with the reference's tolerances.  The
+    reference draws from one mt19937 stream; these are seeded numpy draws of the
+    same distributions.  The 4096^3 case checks 64 sampled rows."""
+    device()
+    print(f"reference cross-check {m}x{n}x{k} {out}", flush=True)
+    g = datagen.rng(900 + m + k, 3)
+    a = g.standard_normal((m, k), dtype=np.float32)
+    w = g.standard_normal((n, k), dtype=np.float32)
+    aq, as_ = oracle.quant(a)
+    bq, bs = oracle.weight_block_quant(w)
+    # the GPU quantizers produce the same bytes and scales
+    q, s = inferop_amd.quantize(to_dev(a))
+    assert np.array_equal(to_np(q), aq)
+    assert np.array_equal(to_np(s).view(np.uint32), as_.view(np.uint32))
+    c = out_to_f32(_gemm(q, s, to_dev(bq), to_dev(bs), m, n, k, out=out))
+    rows = np.arange(m) if m <= 256 else np.unique(
+        np.concatenate([[0, m - 1], g.integers(0, m, 62)]))
+    want = oracle.gemm_rows(aq, as_, bq, bs, rows).astype(np.float64)
+    diff = np.abs(c[rows].astype(np.float64) - want)
+    tol = atol + rtol * np.abs(want)
+    bad = diff > tol
+    assert not bad.any(), (f"{int(bad.sum())}/{bad.size} mismatch, "
+                           f"worst excess {float((diff - tol).max()):.4g}")
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("m", [77, 1000])
 def test_config4_ragged_stress(m):
     device()
