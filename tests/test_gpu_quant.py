@@ -46,7 +46,8 @@ def _assert_same(q, s, qr, sr, what):
 @pytest.mark.parametrize("kind", ["bf16", "fp16", "fp32"])
 @pytest.mark.parametrize("shape,dist", [((16, 1024), "normal"), ((1, 2048), "normal"),
                                         ((64, 7168), "normal"), ((77, 7168), "stress"),
-                                        ((1000, 7168), "stress"), ((3, 128), "normal")])
+                                        ((1000, 7168), "stress"), ((3, 128), "normal"),
+                                        ((64, 768), "normal")])  # tests/test_quant.cpp:11-13
 def test_quant_parity(kind, shape, dist):
     device()
     m, k = shape
