@@ -495,9 +495,11 @@ def main():
         # One GPU's share of a DeepSeek-V3-like MoE layer with 8-way expert
         # parallelism: 32 local experts, gate/up projection (N = 2 x 2048,
         # K = 7168), contiguous layout, rows per expert drawn from a uniform
-        # multinomial routing.  Decode: 64 token-expert rows (the call streams
-        # every expert's weights: GB/s of weight bytes); prefill: 4096 rows
-        # (TFLOP/s).  Two weight copies (1.9 GB) so neither cache holds them.
+        # multinomial routing.  Decode: 64 token-expert rows (GB/s; the call
+        # streams the weights of every expert that has rows, and only those
+        # count: 7 of the 32 experts get none with this seed); prefill: 4096
+        # rows (TFLOP/s).  Two weight copies (1.9 GB) so neither cache holds
+        # them.
         gres = []
         ge_, gn, gk = 32, 4096, 7168
         wsets = [(rand_fp8((ge_, gn, gk)), rand_scales((ge_, gn // 128, gk // 128)))
@@ -519,9 +521,11 @@ def main():
             gg = capture(lambda: [fg(i) for i in range(10)])
             time_graphs([gg], 2)
             us = time_graphs([gg], 5) / 10 * 1e3
-            wbytes = ge_ * gn * gk + 4 * ge_ * (gn // 128) * (gk // 128)
+            used = int((sizes > 0).sum())  # experts whose weights the call reads
+            wbytes = used * (gn * gk + 4 * (gn // 128) * (gk // 128))
             gbytes = wbytes + gm * gk + 4 * gm * (gk // 128) + 2 * gm * gn
-            gres.append({"rows": gm, "experts": ge_, "n": gn, "k": gk, "us": round(us, 2),
+            gres.append({"rows": gm, "experts": ge_, "experts_with_rows": used, "n": gn,
+                         "k": gk, "us": round(us, 2),
                          "gbs": round(gbytes / (us * 1e-6) / 1e9, 1),
                          "hbm_frac": round(gbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                          "tflops": round(2.0 * gm * gn * gk / (us * 1e-6) / 1e12, 1),
