@@ -509,7 +509,10 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_lds_kernel(GemmArgs a) {
 // worth more than preloading for longer K.
 __host__ __device__ constexpr int wide_scale_cap(int) { return 16; }
 
-template <int MT, int WK, int UW, int UA, bool PRE, int OUT_DT>
+// Grouped mode (GROUPED): grid y enumerates virtual M tiles of 16*MT rows as in
+// the tiled kernel's grouped mode (grouped_tile); a workgroup streams one
+// 16-row stripe of its expert's weights against that expert's rows.
+template <int MT, int WK, int UW, int UA, bool PRE, int OUT_DT, bool GROUPED = false>
 __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
   constexpr int kW = 2048;                            // 16 weight rows x 128 B
   constexpr int kCap = wide_scale_cap(MT);
@@ -531,7 +534,21 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
   const int KG = K >> 7;
   const int NB = (N + 127) >> 7;
   const int n0 = blockIdx.x * 16;
-  const int m0 = blockIdx.y * (16 * MT);
+  // activation rows [m0, mend); the expert's weights and scales when grouped
+  int m0, mend;
+  const uint8_t* bq = a.bq;
+  const float* bs = a.bs;
+  if constexpr (GROUPED) {
+    int e, r0, r1;
+    if (!grouped_tile<16 * MT>(a, (int)blockIdx.y, lane, &e, &r0, &r1)) return;
+    m0 = r0;
+    mend = r1;
+    bq += (int64_t)e * N * K;
+    bs += (int64_t)e * NB * KG;
+  } else {
+    m0 = blockIdx.y * (16 * MT);
+    mend = M;
+  }
   const int gw0 = wk * KG / WK, gw1 = (wk + 1) * KG / WK;
   const int cnt = gw1 - gw0;
   const int rsub = lane & 15, c0 = lane >> 4;
@@ -550,10 +567,10 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
 
   if (cnt > 0) {
     // rows past the end of A or B read as zeros
-    const u32x4 rB = rsrc_words(a.bq + (int64_t)n0 * K, (uint32_t)(min(16, N - n0) * K));
-    const u32x4 rA = rsrc_words(a.aq + (int64_t)m0 * K, (uint32_t)(min(16 * MT, M - m0) * K));
-    const float* sb_src = a.bs + (int64_t)min(n0 >> 7, NB - 1) * KG + gw0;
-    const float* sa_src = a.as + (int64_t)(m0 + min(lane % (16 * MT), M - 1 - m0)) * KG + gw0;
+    const u32x4 rB = rsrc_words(bq + (int64_t)n0 * K, (uint32_t)(min(16, N - n0) * K));
+    const u32x4 rA = rsrc_words(a.aq + (int64_t)m0 * K, (uint32_t)(min(16 * MT, mend - m0) * K));
+    const float* sb_src = bs + (int64_t)min(n0 >> 7, NB - 1) * KG + gw0;
+    const float* sa_src = a.as + (int64_t)(m0 + min(lane % (16 * MT), mend - 1 - m0)) * KG + gw0;
     if constexpr (PRE) {
       // entry (r, g) at float r * cnt + g: consecutive lanes read consecutive
       // groups of one activation row
@@ -561,7 +578,7 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
       for (int t = 0; t * 64 < E; ++t) {
         const int idx = min(t * 64 + lane, E - 1);
         const int r = idx / cnt, g = idx - r * cnt;
-        asm_global_to_lds4(a.as + (int64_t)min(m0 + r, M - 1) * KG + gw0 + g, sbase + t * 256);
+        asm_global_to_lds4(a.as + (int64_t)min(m0 + r, mend - 1) * KG + gw0 + g, sbase + t * 256);
       }
       asm_global_to_lds4(sb_src + min(lane, cnt - 1), sbase + kSaF * 4);
     }
@@ -638,11 +655,12 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
     for (int j = wk; j < MT; j += WK) {
       f32x4 s = red[j * 64 + lane];
       for (int w = 1; w < WK; ++w) s += red[(w * MT + j) * 64 + lane];
-      store_out4<OUT_DT>(a, m0 + 16 * j + rsub, n0 + 4 * c0, s);
+      if (m0 + 16 * j + rsub < mend) store_out4<OUT_DT>(a, m0 + 16 * j + rsub, n0 + 4 * c0, s);
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < MT; ++j) store_out4<OUT_DT>(a, m0 + 16 * j + rsub, n0 + 4 * c0, acc[j]);
+    for (int j = 0; j < MT; ++j)
+      if (m0 + 16 * j + rsub < mend) store_out4<OUT_DT>(a, m0 + 16 * j + rsub, n0 + 4 * c0, acc[j]);
   }
 }
 
@@ -1334,6 +1352,10 @@ struct CfgEntry {
   // built (else null); wide decode (kind 4): the variant without the scale
   // preload, for more than wide_scale_cap(MT) groups per wave
   KernelFn fn_alt[3];
+  // wide decode (kind 4): the grouped-expert variants with and without the
+  // scale preload, where built (else null)
+  KernelFn fn_grp[3];
+  KernelFn fn_grp_alt[3];
 };
 
 #define DECODE_CFG(MT, WK, U, NAME)                                                           \
@@ -1374,6 +1396,24 @@ struct CfgEntry {
    {gemm_decode_wide_kernel<MT, WK, UW, UA, false, kFp32>,                                     \
     gemm_decode_wide_kernel<MT, WK, UW, UA, false, kFp16>,                                     \
     gemm_decode_wide_kernel<MT, WK, UW, UA, false, kBf16>}}
+#define DECODE_WIDE_GCFG(MT, WK, UW, UA, NAME)                                                 \
+  {4,                                                                                          \
+   16,                                                                                         \
+   16 * MT,                                                                                    \
+   WK,                                                                                         \
+   NAME,                                                                                       \
+   {gemm_decode_wide_kernel<MT, WK, UW, UA, true, kFp32>,                                      \
+    gemm_decode_wide_kernel<MT, WK, UW, UA, true, kFp16>,                                      \
+    gemm_decode_wide_kernel<MT, WK, UW, UA, true, kBf16>},                                     \
+   {gemm_decode_wide_kernel<MT, WK, UW, UA, false, kFp32>,                                     \
+    gemm_decode_wide_kernel<MT, WK, UW, UA, false, kFp16>,                                     \
+    gemm_decode_wide_kernel<MT, WK, UW, UA, false, kBf16>},                                    \
+   {gemm_decode_wide_kernel<MT, WK, UW, UA, true, kFp32, true>,                                \
+    gemm_decode_wide_kernel<MT, WK, UW, UA, true, kFp16, true>,                                \
+    gemm_decode_wide_kernel<MT, WK, UW, UA, true, kBf16, true>},                               \
+   {gemm_decode_wide_kernel<MT, WK, UW, UA, false, kFp32, true>,                               \
+    gemm_decode_wide_kernel<MT, WK, UW, UA, false, kFp16, true>,                               \
+    gemm_decode_wide_kernel<MT, WK, UW, UA, false, kBf16, true>}}
 #define PERSIST_CFG(BN, BM, WN, WM, NAME)                                                      \
   {3,                                                                                          \
    BN,                                                                                         \
@@ -1409,12 +1449,12 @@ const CfgEntry kCfgs[] = {
     PERSIST_CFG(256, 256, 2, 4, "per_n256_m256_w8"),
     PERSIST_CFG(256, 128, 4, 2, "per_n256_m128_w8"),
     PERSIST_CFG(128, 128, 2, 2, "per_n128_m128_w4"),
-    DECODE_WIDE_CFG(4, 4, 2, 2, "dw_m64_k4_w2a2"),
+    DECODE_WIDE_GCFG(4, 4, 2, 2, "dw_m64_k4_w2a2"),
     DECODE_WIDE_CFG(4, 2, 4, 2, "dw_m64_k2_w4a2"),
-    DECODE_WIDE_CFG(2, 4, 2, 2, "dw_m32_k4_w2a2"),
+    DECODE_WIDE_GCFG(2, 4, 2, 2, "dw_m32_k4_w2a2"),
     DECODE_WIDE_CFG(1, 2, 8, 8, "dw_m16_k2_w8a8"),
-    DECODE_WIDE_CFG(1, 8, 3, 3, "dw_m16_k8_w3a3"),
-    DECODE_WIDE_CFG(1, 4, 3, 3, "dw_m16_k4_w3a3"),
+    DECODE_WIDE_GCFG(1, 8, 3, 3, "dw_m16_k8_w3a3"),
+    DECODE_WIDE_GCFG(1, 4, 3, 3, "dw_m16_k4_w3a3"),
     DECODE_WIDE_CFG(1, 8, 2, 2, "dw_m16_k8_w2a2"),
 };
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
@@ -1521,7 +1561,8 @@ extern "C" int inferop_hip_gemm_config_info(int32_t cfg, inferop_gemm_cfg_info* 
   info->waves = kCfgs[cfg].waves;
   info->kind = kCfgs[cfg].kind;
   info->name = kCfgs[cfg].name;
-  info->grouped = (kCfgs[cfg].kind == 2 || kCfgs[cfg].kind == 3) && kCfgs[cfg].fn_alt[0] != nullptr;
+  info->grouped = ((kCfgs[cfg].kind == 2 || kCfgs[cfg].kind == 3) && kCfgs[cfg].fn_alt[0]) ||
+                  (kCfgs[cfg].kind == 4 && kCfgs[cfg].fn_grp[0]);
   return hipSuccess;
 }
 
@@ -1605,7 +1646,9 @@ extern "C" int inferop_hip_gemm_w8a8_block_grouped(void* c, const uint8_t* a_q,
   const int di = dt_index(out_dt);
   if (di < 0 || cfg < 0 || cfg >= kNumCfgs) return hipErrorInvalidValue;
   const CfgEntry& cf = kCfgs[cfg];
-  if ((cf.kind != 2 && cf.kind != 3) || !cf.fn_alt[di]) return hipErrorInvalidValue;
+  const bool grp_ok = ((cf.kind == 2 || cf.kind == 3) && cf.fn_alt[di]) ||
+                      (cf.kind == 4 && cf.fn_grp[di] && cf.fn_grp_alt[di]);
+  if (!grp_ok) return hipErrorInvalidValue;
   if (cf.kind == 3 && (k / 128) % 2 != 0) return hipErrorInvalidValue;
   if (m < 0 || n <= 0 || k <= 0 || k % 128 != 0 || experts <= 0 || max_m < 0)
     return hipErrorInvalidValue;
@@ -1616,9 +1659,12 @@ extern "C" int inferop_hip_gemm_w8a8_block_grouped(void* c, const uint8_t* a_q,
     return hipErrorInvalidValue;
   // tile rows are addressed with 32-bit buffer offsets
   if ((int64_t)(cf.bn > cf.bm ? cf.bn : cf.bm) * k > 0x7FFFFFFF) return hipErrorInvalidValue;
-  // every expert's M tiles fit in ceil(m / BM) + experts virtual tiles
+  // every expert's M tiles fit in ceil(m / BM) + min(experts, m) virtual
+  // tiles (an expert's last tile holds at least one of its rows; with
+  // overlapping out-of-range offsets some tiles may fall outside the grid,
+  // which leaves outputs unwritten but never addresses outside A, B or C)
   const int64_t tn = (n + cf.bn - 1) / cf.bn;
-  const int64_t tmv = (m + cf.bm - 1) / cf.bm + experts;
+  const int64_t tmv = (m + cf.bm - 1) / cf.bm + (experts < m ? experts : m);
   if (tn * tmv > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int out_bytes = out_dt == kFp32 ? 4 : 2;
@@ -1626,6 +1672,14 @@ extern "C" int inferop_hip_gemm_w8a8_block_grouped(void* c, const uint8_t* a_q,
   GemmArgs args{c,      a_q,    a_scales,     b_q,         b_scales,
                 nullptr, nullptr, (int)m,     (int)n,      (int)k,
                 vec_ok, offsets, (int)experts, (int)max_m};
+  if (cf.kind == 4) {
+    // one workgroup per (16-row weight stripe, virtual M tile of the experts)
+    if (16 * k > 0x7FFFFFFF || tmv > 65535) return hipErrorInvalidConfiguration;
+    const int64_t per_wave = (k / 128 + cf.waves - 1) / cf.waves;
+    const KernelFn fn = per_wave <= wide_scale_cap(cf.bm / 16) ? cf.fn_grp[di] : cf.fn_grp_alt[di];
+    hipLaunchKernelGGL(fn, dim3((unsigned)tn, (unsigned)tmv), dim3(64 * cf.waves), 0, st, args);
+    return hipGetLastError();
+  }
   int64_t grid = tn * tmv;
   if (cf.kind == 3) {
     // persistent: one workgroup per CU (two for 128x128 tiles) walks the

@@ -342,7 +342,13 @@ int gemm_impl(void* c, const void* a_q, const void* a_scales, const void* b_q,
 }
 
 // Grouped (MoE expert) GEMM: the configuration from the mean rows per expert.
-// With an even K / 128 the persistent kernels, whose load pipeline runs on
+// Up to 8 rows per expert (decode routings) the wide decode kernel: one
+// workgroup per (16-row weight stripe, expert tile) streams the stripe over
+// the whole K range, so the weights of every expert with rows leave HBM once
+// at the decode kernel's rate (32 experts, N=4096, K=7168: 2 rows per expert
+// 124 us vs 154 us on the persistent 128x128 tiles, 8 rows 165 vs 173 us; at
+// 16 rows 243 vs 174 us).  Beyond that, with an even K / 128, the persistent
+// kernels, whose load pipeline runs on
 // across a workgroup's tiles, stream the experts' weights best whatever the
 // rows: two 128x128 workgroups per CU below about 96 rows per expert, one
 // 256x256 beyond (measured at 32 experts, N=4096, K=7168: 2 rows per expert
@@ -353,6 +359,8 @@ int gemm_impl(void* c, const void* a_q, const void* a_scales, const void* b_q,
 // below 24, 64-row three-stage below 64, 128x128 beyond.
 int32_t select_grouped(int64_t m, int64_t k, int64_t num_experts) {
   const int64_t avg = m / (num_experts > 0 ? num_experts : 1);
+  const int64_t ne = num_experts < m ? num_experts : m;
+  if (avg <= 8 && 16 * k <= 0x7FFFFFFF && (m + 15) / 16 + ne <= 65535) return kDwM16K4;
   if ((k / 128) % 2 == 0) return avg < 96 ? kPerN128M128 : kPerN256M256;
   if (avg < 16) return kPreN128M16S4;
   if (avg < 24) return kPreN128M32S4;

@@ -21,7 +21,8 @@ DT = inferop_amd.dtype
 TORCH_OUT = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}
 N_CONFIGS = inferop_amd.gemm_num_configs()
 GROUPED = ["pre_n128_m128_w4_s2", "pre_n128_m64_w8_s4", "pre_n128_m32_w8_s4", "pre_n128_m16_w8_s4",
-           "pre_n128_m64_w8_s3", "per_n256_m256_w8", "per_n256_m128_w8", "per_n128_m128_w4"]
+           "pre_n128_m64_w8_s3", "per_n256_m256_w8", "per_n256_m128_w8", "per_n128_m128_w4",
+           "dw_m16_k8_w3a3", "dw_m16_k4_w3a3", "dw_m32_k4_w2a2", "dw_m64_k4_w2a2"]
 
 
 def _cfg(name):

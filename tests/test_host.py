@@ -214,7 +214,8 @@ def test_grouped_gemm_host_checks():
     for i, name in enumerate(names):
         if name not in ("pre_n128_m128_w4_s2", "pre_n128_m64_w8_s4", "pre_n128_m32_w8_s4",
                         "pre_n128_m16_w8_s4", "pre_n128_m64_w8_s3", "per_n256_m256_w8",
-                        "per_n256_m128_w8", "per_n128_m128_w4"):
+                        "per_n256_m128_w8", "per_n128_m128_w4", "dw_m16_k8_w3a3",
+                        "dw_m16_k4_w3a3", "dw_m32_k4_w2a2", "dw_m64_k4_w2a2"):
             assert gc(0, 0, 0, 0, 0, 0, 16, 512, 1024, 8, inferop_amd.dtype.bf16, i) == \
                 S.ERR_ARGUMENT, name
     gm = inferop_amd.w8a8_block_fp8_grouped_gemm_masked
@@ -230,11 +231,15 @@ def test_grouped_gemm_host_checks():
               names.index("per_n256_m256_w8")) == S.ERR_ARGUMENT
     # even K / 128: the persistent kernels; odd: the tiled ones
     sel = lambda m, e: names[inferop_amd.grouped_gemm_select(m, 4096, 7168, e)]
-    assert sel(64 * 8, 256) == "per_n128_m128_w4"
+    # up to 8 rows per expert: the wide decode kernel over (stripe, expert tile)
+    assert sel(64 * 8, 256) == "dw_m16_k4_w3a3"
+    assert sel(8 * 32, 32) == "dw_m16_k4_w3a3"
+    assert sel(9 * 32, 32) == "per_n128_m128_w4"
     assert sel(64 * 256, 256) == "per_n128_m128_w4"
     assert sel(128 * 256, 256) == "per_n256_m256_w8"
     sel = lambda m, e: names[inferop_amd.grouped_gemm_select(m, 4096, 7168 + 128, e)]
-    assert sel(64 * 8, 256) == "pre_n128_m16_w8_s4"
+    assert sel(64 * 8, 256) == "dw_m16_k4_w3a3"
+    assert sel(12 * 256, 256) == "pre_n128_m16_w8_s4"
     assert sel(20 * 256, 256) == "pre_n128_m32_w8_s4"
     assert sel(32 * 256, 256) == "pre_n128_m64_w8_s3"
     assert sel(64 * 256, 256) == "pre_n128_m128_w4_s2"
