@@ -349,7 +349,20 @@ __global__ __launch_bounds__(256) void weight_block_quant_kernel(uint8_t* __rest
   const int64_t kg = k >> 7;
   const int64_t g = blockIdx.x, nb = blockIdx.y;
   const int64_t col = g * 128 + c * 8;
-  float v[kRows][8];
+  // the block's values stay in registers as loaded (16-bit inputs packed two
+  // to a word: half the registers of fp32 copies, so more workgroups per CU)
+  constexpr int W = DT == kFp32 ? 8 : 4;
+  uint32_t wv[kRows][W];
+  auto val = [&](int i, int j) -> float {
+    if constexpr (DT == kFp32) {
+      return u2f(wv[i][j]);
+    } else if constexpr (DT == kBf16) {
+      return u2f((j & 1) ? (wv[i][j >> 1] & 0xFFFF0000u) : (wv[i][j >> 1] << 16));
+    } else {
+      return (float)__builtin_bit_cast(
+          _Float16, (uint16_t)((j & 1) ? (wv[i][j >> 1] >> 16) : (wv[i][j >> 1] & 0xFFFFu)));
+    }
+  };
   uint32_t key = 0;
 #pragma unroll
   for (int i = 0; i < kRows; ++i) {
@@ -359,29 +372,25 @@ __global__ __launch_bounds__(256) void weight_block_quant_kernel(uint8_t* __rest
       if constexpr (DT == kFp32) {
         const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(w) + e);
         const u32x4 a = p[0], b = p[1];
-        const uint32_t ws[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[i][j] = u2f(ws[j]);
+        wv[i][0] = a.x, wv[i][1] = a.y, wv[i][2] = a.z, wv[i][3] = a.w;
+        wv[i][4] = b.x, wv[i][5] = b.y, wv[i][6] = b.z, wv[i][7] = b.w;
       } else {
         const u32x4 a = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(w) + e);
-        const uint32_t ws[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if constexpr (DT == kBf16) {
-            v[i][2 * j] = u2f(ws[j] << 16);
-            v[i][2 * j + 1] = u2f(ws[j] & 0xFFFF0000u);
-          } else {
-            v[i][2 * j] = (float)__builtin_bit_cast(_Float16, (uint16_t)ws[j]);
-            v[i][2 * j + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(ws[j] >> 16));
-          }
-        }
+        wv[i][0] = a.x, wv[i][1] = a.y, wv[i][2] = a.z, wv[i][3] = a.w;
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[i][j] = 0.0f;
+      for (int j = 0; j < W; ++j) wv[i][j] = 0u;
     }
+    if constexpr (DT == kBf16) {
+      // |value| bits straight from the packed words (no fp32 copies kept)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) key = max(key, f2u(v[i][j]) & 0x7FFFFFFFu);
+      for (int j = 0; j < 4; ++j)
+        key = max(key, max((wv[i][j] << 16) & 0x7FFFFFFFu, wv[i][j] & 0x7FFF0000u));
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) key = max(key, f2u(val(i, j)) & 0x7FFFFFFFu);
+    }
   }
   key = block_max_u32(key, red);
   const bool slow = key >= 0x7F800000u || (key != 0 && key < kFastMinAbsmaxBits);
@@ -393,27 +402,63 @@ __global__ __launch_bounds__(256) void weight_block_quant_kernel(uint8_t* __rest
     for (int i = 0; i < kRows; ++i) {
       const int64_t row = nb * 128 + (t >> 4) + 16 * i;
       if (row < n) {
-        const uint32_t lo = cvt_pk4_e4m3(v[i][0] * inv, v[i][1] * inv, v[i][2] * inv, v[i][3] * inv);
-        const uint32_t hi = cvt_pk4_e4m3(v[i][4] * inv, v[i][5] * inv, v[i][6] * inv, v[i][7] * inv);
+        const uint32_t lo = cvt_pk4_e4m3(val(i, 0) * inv, val(i, 1) * inv, val(i, 2) * inv, val(i, 3) * inv);
+        const uint32_t hi = cvt_pk4_e4m3(val(i, 4) * inv, val(i, 5) * inv, val(i, 6) * inv, val(i, 7) * inv);
         *reinterpret_cast<u32x2*>(q + row * k + col) = u32x2{lo, hi};
       }
     }
   } else {
+    // rare blocks (Inf/NaN or a tiny absmax): the rows are read again from
+    // memory one at a time, so this path holds no block copy in registers
+    auto row_vals = [&](int i, float* x) {
+      const int64_t row = nb * 128 + (t >> 4) + 16 * i;
+      if (row >= n) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = 0.0f;
+        return;
+      }
+      const int64_t e = row * k + col;
+      if constexpr (DT == kFp32) {
+        const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(w) + e);
+        const u32x4 a = p[0], b = p[1];
+        const uint32_t r[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = u2f(r[j]);
+      } else {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(w) + e);
+        const uint32_t r[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if constexpr (DT == kBf16) {
+            x[2 * j] = u2f(r[j] << 16);
+            x[2 * j + 1] = u2f(r[j] & 0xFFFF0000u);
+          } else {
+            x[2 * j] = (float)__builtin_bit_cast(_Float16, (uint16_t)(r[j] & 0xFFFFu));
+            x[2 * j + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(r[j] >> 16));
+          }
+        }
+      }
+    };
     uint32_t k2 = 0;
+#pragma unroll 1
+    for (int i = 0; i < kRows; ++i) {
+      float x[8];
+      row_vals(i, x);
 #pragma unroll
-    for (int i = 0; i < kRows; ++i)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) k2 = max(k2, mag_nonan(v[i][j]));
+      for (int j = 0; j < 8; ++j) k2 = max(k2, mag_nonan(x[j]));
+    }
     k2 = block_max_u32(k2, red);
     s = (k2 == 0) ? 1.0f : u2f(k2) * kInv448;
     const float inv = 1.0f / s;
-#pragma unroll
+#pragma unroll 1
     for (int i = 0; i < kRows; ++i) {
       const int64_t row = nb * 128 + (t >> 4) + 16 * i;
       if (row < n) {
+        float x[8];
+        row_vals(i, x);
         uint32_t cd[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) cd[j] = slow_code_mul(v[i][j], inv);
+        for (int j = 0; j < 8; ++j) cd[j] = slow_code_mul(x[j], inv);
         *reinterpret_cast<u32x2*>(q + row * k + col) =
             u32x2{cd[0] | (cd[1] << 8) | (cd[2] << 16) | (cd[3] << 24),
                   cd[4] | (cd[5] << 8) | (cd[6] << 16) | (cd[7] << 24)};
