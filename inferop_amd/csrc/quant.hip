@@ -271,12 +271,21 @@ hipError_t launch_quant(void* q, float* scales, const void* x, int64_t rows, int
   const int64_t ngroups = rows * (cols / gs);
   const bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)q % 8 == 0) && ((uintptr_t)scales % 4 == 0);
   if (gs == 128 && aligned) {
-    constexpr int U = 2;
-    const int64_t per_block = 16 * U;
-    const int64_t blocks = (ngroups + per_block - 1) / per_block;
-    if (blocks > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL((quant_g128_kernel<DT, U>), dim3((unsigned)blocks), dim3(256), 0, st,
-                       (uint8_t*)q, scales, (const uint32_t*)x, ngroups);
+    // two groups per lane for large inputs (4096x7168: 16.1 us vs 18.4 with
+    // one); one for decode-sized inputs, where the launch has fewer groups
+    // than the GPU has lanes to spread them over (64x7168: 2.5 vs 2.8 us)
+    if (ngroups <= 16384) {
+      const int64_t blocks = (ngroups + 15) / 16;
+      hipLaunchKernelGGL((quant_g128_kernel<DT, 1>), dim3((unsigned)blocks), dim3(256), 0, st,
+                         (uint8_t*)q, scales, (const uint32_t*)x, ngroups);
+    } else {
+      constexpr int U = 2;
+      const int64_t per_block = 16 * U;
+      const int64_t blocks = (ngroups + per_block - 1) / per_block;
+      if (blocks > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
+      hipLaunchKernelGGL((quant_g128_kernel<DT, U>), dim3((unsigned)blocks), dim3(256), 0, st,
+                         (uint8_t*)q, scales, (const uint32_t*)x, ngroups);
+    }
   } else {
     int64_t blocks = (ngroups + 3) / 4;
     if (blocks > 65536) blocks = 65536;
