@@ -272,9 +272,10 @@ hipError_t launch_quant(void* q, float* scales, const void* x, int64_t rows, int
   const bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)q % 8 == 0) && ((uintptr_t)scales % 4 == 0);
   if (gs == 128 && aligned) {
     // two groups per lane for large inputs (4096x7168: 16.1 us vs 18.4 with
-    // one); one for decode-sized inputs, where the launch has fewer groups
-    // than the GPU has lanes to spread them over (64x7168: 2.5 vs 2.8 us)
-    if (ngroups <= 16384) {
+    // one; 1024x7168: 5.6 vs 6.2 us); one up to 32768 groups, where the
+    // launch has few groups to spread over the GPU (64x7168: 2.5 vs 2.8 us,
+    // 512x7168: 3.6 vs 3.9 us)
+    if (ngroups <= 32768) {
       const int64_t blocks = (ngroups + 15) / 16;
       hipLaunchKernelGGL((quant_g128_kernel<DT, 1>), dim3((unsigned)blocks), dim3(256), 0, st,
                          (uint8_t*)q, scales, (const uint32_t*)x, ngroups);
