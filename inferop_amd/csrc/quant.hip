@@ -600,8 +600,13 @@ __global__ __launch_bounds__(256) void add_rmsnorm_quant_kernel(
   const int64_t row = blockIdx.x;
   uint8_t* res = reinterpret_cast<uint8_t*>(residual) + row * cols * EB;
   const uint8_t* xr = reinterpret_cast<const uint8_t*>(x) + row * cols * EB;
+  // pass 1 stores residual = dt(residual + x) and sums the squares of the
+  // stored values; the first kKeep column blocks (cols <= 8192) keep those
+  // values in registers for pass 2, longer rows read the rest back
+  constexpr int kKeep = 4;
+  float keep[kKeep][8];
   float ss = 0.0f;
-  for (int64_t c = (int64_t)t * 8; c < cols; c += 2048) {
+  auto pass1 = [&](int64_t c, float* stored) {
     float rv[8], xv[8];
     load_dt8<DT>(res + c * EB, rv);
     load_dt8<DT>(xr + c * EB, xv);
@@ -615,10 +620,18 @@ __global__ __launch_bounds__(256) void add_rmsnorm_quant_kernel(
     } else {
       *reinterpret_cast<u32x4*>(res + c * EB) = u32x4{w[0], w[1], w[2], w[3]};
     }
-    float stored[8];
     load_dt8<DT>(w, stored);
 #pragma unroll
     for (int i = 0; i < 8; ++i) ss += stored[i] * stored[i];
+  };
+#pragma unroll
+  for (int it = 0; it < kKeep; ++it) {
+    const int64_t c = (int64_t)t * 8 + it * 2048;
+    if (c < cols) pass1(c, keep[it]);
+  }
+  for (int64_t c = (int64_t)t * 8 + kKeep * 2048; c < cols; c += 2048) {
+    float stored[8];
+    pass1(c, stored);
   }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
@@ -628,13 +641,20 @@ __global__ __launch_bounds__(256) void add_rmsnorm_quant_kernel(
   const float inv = 1.0f / __builtin_sqrtf(ss / (float)cols + eps);
   const int64_t gpr = cols >> 7;
   const uint8_t* wt = reinterpret_cast<const uint8_t*>(weight);
-  for (int64_t c0 = 0; c0 < cols; c0 += 2048) {
+  // pass 2: out = dt((residual * inv) * weight), quantized per 128 columns;
+  // kept values come from registers, the rest from this thread's own stores
+  auto pass2 = [&](int64_t c0, const float* kept) {
     const int64_t c = c0 + (int64_t)t * 8;
     const bool live = c < cols;  // whole 16-lane groups, since cols % 128 == 0
     float y[8];
     if (live) {
       float rv[8], wv[8];
-      load_dt8<DT>(res + c * EB, rv);  // this thread's own stores above
+      if (kept) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) rv[i] = kept[i];
+      } else {
+        load_dt8<DT>(res + c * EB, rv);
+      }
       load_dt8<DT>(wt + c * EB, wv);
 #pragma unroll
       for (int i = 0; i < 8; ++i) y[i] = rv[i] * inv * wv[i];
@@ -651,7 +671,11 @@ __global__ __launch_bounds__(256) void add_rmsnorm_quant_kernel(
       *reinterpret_cast<u32x2*>(q + row * cols + c) = u32x2{lo, hi};
       if ((t & 15) == 0) scales[row * gpr + (c >> 7)] = s;
     }
-  }
+  };
+#pragma unroll
+  for (int it = 0; it < kKeep; ++it)
+    if (it * 2048 < cols) pass2(it * 2048, keep[it]);
+  for (int64_t c0 = kKeep * 2048; c0 < cols; c0 += 2048) pass2(c0, nullptr);
 }
 
 template <int DT>
