@@ -110,6 +110,8 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(int32_t* __restrict__
   uint32_t prev_b = 0xFFFFFFFFu;  // above every probability
   int prev_e = -1;
   float wsum = 0.0f;
+  int32_t my_id = 0;
+  float my_w = 0.0f;
   for (int k = 0; k < topk; ++k) {
     uint32_t key = 0;
 #pragma unroll
@@ -132,13 +134,25 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(int32_t* __restrict__
     prev_b = bb;
     prev_e = be;
     const float wk = u2f(bb) / l;
-    if (lane == 0) {
+    if (topk <= 64) {
+      // lane k keeps choice k; the row is stored once at the end
+      if (lane == k) {
+        my_id = be;
+        my_w = wk;
+      }
+    } else if (lane == 0) {
       tid[k] = be;
       tw[k] = wk;
     }
     wsum += wk;  // every lane holds the same left-to-right sum
   }
-  if (renormalize && wsum > 0.0f && lane == 0) {
+  const bool renorm = renormalize && wsum > 0.0f;
+  if (topk <= 64) {
+    if (lane < topk) {
+      tid[lane] = my_id;
+      tw[lane] = renorm ? my_w / wsum : my_w;
+    }
+  } else if (renorm && lane == 0) {
     for (int k = 0; k < topk; ++k) tw[k] = tw[k] / wsum;
   }
 }
