@@ -137,6 +137,10 @@ int inferop_w8a8_block_fp8_grouped_gemm_config(void* c, const void* a_q, const v
                                                int32_t out_dt, int32_t config, void* stream);
 int inferop_grouped_gemm_select(int64_t m, int64_t n, int64_t k, int64_t num_experts,
                                 int32_t* config);
+/* The configuration the masked grouped GEMM would choose for these
+ * arguments (expected_m as in inferop_w8a8_block_fp8_grouped_gemm_masked). */
+int inferop_grouped_gemm_masked_select(int64_t max_m, int64_t n, int64_t k, int64_t num_experts,
+                                       int64_t expected_m, int32_t* config);
 int inferop_w8a8_block_fp8_grouped_gemm_masked_config(void* c, const void* a_q,
                                                       const void* a_scales, const void* b_q,
                                                       const void* b_scales,

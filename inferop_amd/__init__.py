@@ -9,8 +9,8 @@ from ._lib import LIB_PATH, LibraryNotBuilt, lib  # noqa: F401
 from .ops import (  # noqa: F401
     InferopError, Status, dequant_fp8_per_token_group, dequantize, device_count, device_name,
     device_sm_version, dtype, fused_add_rmsnorm_quant_fp8, gemm, gemm_config_name,
-    gemm_num_configs, gemm_select, grouped_gemm_select, has_cuda, silu_and_mul_quant_fp8,
-    topk_softmax, quant_fp8_per_token_group, quant_fp8_weight_block, quantize, quantize_weight,
-    w8a8_block_fp8_gemm, w8a8_block_fp8_gemm_config, w8a8_block_fp8_grouped_gemm,
+    gemm_num_configs, gemm_select, grouped_gemm_masked_select, grouped_gemm_select, has_cuda,
+    silu_and_mul_quant_fp8, topk_softmax, quant_fp8_per_token_group, quant_fp8_weight_block,
+    quantize, quantize_weight, w8a8_block_fp8_gemm, w8a8_block_fp8_gemm_config, w8a8_block_fp8_grouped_gemm,
     w8a8_block_fp8_grouped_gemm_config, w8a8_block_fp8_grouped_gemm_masked,
     w8a8_block_fp8_grouped_gemm_masked_config)

@@ -47,6 +47,7 @@ C_API = [
     ("inferop_w8a8_block_fp8_grouped_gemm_config", ctypes.c_int,
      [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i32, _vp]),
     ("inferop_grouped_gemm_select", ctypes.c_int, [_i64, _i64, _i64, _i64, _vp]),
+    ("inferop_grouped_gemm_masked_select", ctypes.c_int, [_i64, _i64, _i64, _i64, _i64, _vp]),
     ("inferop_w8a8_block_fp8_grouped_gemm_masked_config", ctypes.c_int,
      [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i32, _vp]),
     ("inferop_gemm_select", ctypes.c_int,

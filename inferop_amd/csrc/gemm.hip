@@ -1460,63 +1460,97 @@ const CfgEntry kCfgs[] = {
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
 // ---- split-K workspace, one per (device, stream) ------------------------------
+// Fixed capacity: INFEROP_SPLITK_WS_BYTES of fp32 partials and
+// INFEROP_SPLITK_WS_COUNTERS arrival counters, allocated at a stream's first
+// split-K call and kept until the process ends -- never grown, replaced or
+// freed, so a HIP graph captured on the stream keeps valid pointers and no
+// call waits for the host.  The automatic tile choice stays within the
+// capacity; a forced split that needs more is rejected before any launch.
+// The counters start at zero and every launch leaves them at zero (the
+// workgroup that completes a tile resets its counter).
 
 __global__ void fill_zero_kernel(int* p, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i < n) p[i] = 0;
 }
 
+hipError_t launch_fill_zero(int* p, int64_t n, hipStream_t st) {
+  hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p, n);
+  return hipGetLastError();
+}
+
 struct Workspace {
-  float* partials = nullptr;
-  size_t partial_bytes = 0;
-  int* counters = nullptr;
-  size_t counter_count = 0;
+  float* partials;
+  int* counters;
 };
 
 std::mutex g_ws_mutex;
-std::unordered_map<uint64_t, Workspace> g_ws;
+std::unordered_map<uint64_t, Workspace> g_ws;  // entries are never changed or erased
+hipStream_t g_zero_stream[64];                 // per device, for captured first calls
 
-hipError_t get_workspace(hipStream_t st, size_t partial_bytes, size_t counters, float** ws,
-                         int** cnt) {
+hipError_t get_workspace(hipStream_t st, float** ws, int** cnt) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
   const uint64_t key = (uint64_t)(uintptr_t)st * 64u + (uint64_t)dev;
   std::lock_guard<std::mutex> lock(g_ws_mutex);
-  Workspace& w = g_ws[key];
-  if (w.partial_bytes < partial_bytes) {
-    if (w.partials) {
-      e = hipStreamSynchronize(st);
-      if (e != hipSuccess) return e;
-      (void)hipFree(w.partials);
-      w.partials = nullptr;
-      w.partial_bytes = 0;
-    }
-    const size_t bytes = partial_bytes + partial_bytes / 2;
-    e = hipMalloc(&w.partials, bytes);
-    if (e != hipSuccess) return e;
-    w.partial_bytes = bytes;
+  auto it = g_ws.find(key);
+  if (it != g_ws.end()) {
+    *ws = it->second.partials;
+    *cnt = it->second.counters;
+    return hipSuccess;
   }
-  if (w.counter_count < counters) {
-    if (w.counters) {
-      e = hipStreamSynchronize(st);
-      if (e != hipSuccess) return e;
-      (void)hipFree(w.counters);
-      w.counters = nullptr;
-      w.counter_count = 0;
-    }
-    const size_t count = counters < 4096 ? 4096 : counters * 2;
-    e = hipMalloc(&w.counters, count * sizeof(int));
+  // First split-K call on this stream.  While the stream is being captured,
+  // hipMalloc is only allowed in relaxed capture mode, and the counters are
+  // zeroed on a library stream that is not captured (waited for here, once);
+  // otherwise the zeroing kernel runs on the caller's stream ahead of the GEMM.
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  e = hipStreamIsCapturing(st, &cs);
+  if (e != hipSuccess) return e;
+  const bool capturing = cs != hipStreamCaptureStatusNone;
+  hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+  if (capturing) {
+    e = hipThreadExchangeStreamCaptureMode(&mode);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, st,
-                       w.counters, (int64_t)count);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    w.counter_count = count;
   }
-  *ws = w.partials;
-  *cnt = w.counters;
+  char* base = nullptr;
+  const size_t bytes = (size_t)INFEROP_SPLITK_WS_BYTES + (size_t)INFEROP_SPLITK_WS_COUNTERS * 4;
+  e = hipMalloc(&base, bytes);
+  int* counters = reinterpret_cast<int*>(base + INFEROP_SPLITK_WS_BYTES);
+  if (e == hipSuccess) {
+    if (capturing) {
+      if (!g_zero_stream[dev]) e = hipStreamCreateWithFlags(&g_zero_stream[dev], hipStreamNonBlocking);
+      if (e == hipSuccess) e = launch_fill_zero(counters, INFEROP_SPLITK_WS_COUNTERS, g_zero_stream[dev]);
+      if (e == hipSuccess) e = hipStreamSynchronize(g_zero_stream[dev]);
+    } else {
+      e = launch_fill_zero(counters, INFEROP_SPLITK_WS_COUNTERS, st);
+    }
+  }
+  if (capturing) {
+    const hipError_t e2 = hipThreadExchangeStreamCaptureMode(&mode);
+    if (e == hipSuccess) e = e2;
+  }
+  // a failed set-up keeps its memory (it may be in use by a launched fill)
+  if (e != hipSuccess) return e;
+  g_ws.emplace(key, Workspace{reinterpret_cast<float*>(base), counters});
+  *ws = reinterpret_cast<float*>(base);
+  *cnt = counters;
   return hipSuccess;
+}
+
+// Workspace a launch of configuration cf with `split` K partitions needs
+// (0 without a split), and whether it fits the fixed capacity.
+int64_t workspace_bytes(const CfgEntry& cf, int64_t split, int64_t m, int64_t n) {
+  if (split <= 1 || cf.kind == 3 || cf.kind == 4) return 0;
+  const int64_t tiles = ((n + cf.bn - 1) / cf.bn) * ((m + cf.bm - 1) / cf.bm);
+  return split * tiles * cf.bn * cf.bm * 4;
+}
+bool workspace_fits(const CfgEntry& cf, int64_t split, int64_t m, int64_t n) {
+  if (split <= 1 || cf.kind == 3 || cf.kind == 4) return true;
+  const int64_t tiles = ((n + cf.bn - 1) / cf.bn) * ((m + cf.bm - 1) / cf.bm);
+  return tiles <= INFEROP_SPLITK_WS_COUNTERS &&
+         workspace_bytes(cf, split, m, n) <= (int64_t)INFEROP_SPLITK_WS_BYTES;
 }
 
 // Compute units of the current device (cached per device ordinal).
@@ -1566,10 +1600,22 @@ extern "C" int inferop_hip_gemm_config_info(int32_t cfg, inferop_gemm_cfg_info* 
   return hipSuccess;
 }
 
-extern "C" int inferop_hip_gemm_w8a8_block(void* c, const uint8_t* a_q, const float* a_scales,
-                                           const uint8_t* b_q, const float* b_scales, int64_t m,
-                                           int64_t n, int64_t k, int32_t out_dt,
-                                           const inferop_gemm_launch* launch, void* stream) {
+extern "C" int64_t inferop_hip_gemm_workspace_bytes(int32_t cfg, int32_t split, int64_t m,
+                                                    int64_t n, int64_t k) {
+  if (cfg < 0 || cfg >= kNumCfgs || m <= 0 || n <= 0 || k < 128) return -1;
+  int64_t s = split < 1 ? 1 : split;
+  if (s > k / 128) s = k / 128;
+  const CfgEntry& cf = kCfgs[cfg];
+  const int64_t tiles = ((n + cf.bn - 1) / cf.bn) * ((m + cf.bm - 1) / cf.bm);
+  if (s > 1 && cf.kind != 3 && cf.kind != 4 && tiles > INFEROP_SPLITK_WS_COUNTERS) return -1;
+  return workspace_bytes(cf, s, m, n);
+}
+
+namespace inferop_hip {
+namespace {
+int gemm_block(void* c, const uint8_t* a_q, const float* a_scales, const uint8_t* b_q,
+               const float* b_scales, int64_t m, int64_t n, int64_t k, int32_t out_dt,
+               const inferop_gemm_launch* launch, void* stream) {
   const int di = dt_index(out_dt);
   if (di < 0 || !launch || launch->cfg < 0 || launch->cfg >= kNumCfgs) return hipErrorInvalidValue;
   if (m <= 0 || n <= 0 || k <= 0 || k % 128 != 0) return hipErrorInvalidValue;
@@ -1589,10 +1635,9 @@ extern "C" int inferop_hip_gemm_w8a8_block(void* c, const uint8_t* a_q, const fl
     int split = launch->split_k < 1 ? 1 : launch->split_k;
     if (split > kg) split = kg;
     if (tn > 0x7FFFFFFF || split > 65535 || tm > 65535) return hipErrorInvalidConfiguration;
+    if (!workspace_fits(cf, split, m, n)) return hipErrorInvalidValue;
     if (split > 1) {
-      const size_t tiles = (size_t)(tn * tm);
-      const size_t bytes = (size_t)split * tiles * (size_t)cf.bn * (size_t)cf.bm * sizeof(float);
-      hipError_t e = get_workspace(st, bytes, tiles, &args.ws, &args.counters);
+      hipError_t e = get_workspace(st, &args.ws, &args.counters);
       if (e != hipSuccess) return e;
     }
     hipLaunchKernelGGL(cf.fn[di], dim3((unsigned)tn, (unsigned)split, (unsigned)tm),
@@ -1626,15 +1671,24 @@ extern "C" int inferop_hip_gemm_w8a8_block(void* c, const uint8_t* a_q, const fl
     if (tiles > 0x7FFFFFFF || split > 65535) return hipErrorInvalidConfiguration;
     // tile rows are addressed with 32-bit buffer offsets
     if ((int64_t)(cf.bn > cf.bm ? cf.bn : cf.bm) * k > 0x7FFFFFFF) return hipErrorInvalidValue;
+    if (!workspace_fits(cf, split, m, n)) return hipErrorInvalidValue;
     if (split > 1) {
-      const size_t bytes = (size_t)split * (size_t)tiles * (size_t)cf.bn * (size_t)cf.bm * 4;
-      hipError_t e = get_workspace(st, bytes, (size_t)tiles, &args.ws, &args.counters);
+      hipError_t e = get_workspace(st, &args.ws, &args.counters);
       if (e != hipSuccess) return e;
     }
     hipLaunchKernelGGL(cf.fn[di], dim3((unsigned)tiles, (unsigned)split), dim3(64 * cf.waves), 0,
                        st, args);
   }
   return hipGetLastError();
+}
+}  // namespace
+}  // namespace inferop_hip
+
+extern "C" int inferop_hip_gemm_w8a8_block(void* c, const uint8_t* a_q, const float* a_scales,
+                                           const uint8_t* b_q, const float* b_scales, int64_t m,
+                                           int64_t n, int64_t k, int32_t out_dt,
+                                           const inferop_gemm_launch* launch, void* stream) {
+  return gemm_block(c, a_q, a_scales, b_q, b_scales, m, n, k, out_dt, launch, stream);
 }
 
 extern "C" int inferop_hip_gemm_w8a8_block_grouped(void* c, const uint8_t* a_q,

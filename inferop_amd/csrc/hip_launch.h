@@ -64,8 +64,20 @@ typedef struct {
   int32_t grouped; /* kind 2: has a grouped-expert variant */
 } inferop_gemm_cfg_info;
 
+/* Capacity of the split-K workspace the library keeps per (device, stream):
+ * fp32 partial bytes and arrival counters (one per output tile).  A launch
+ * whose split needs more is rejected with hipErrorInvalidValue. */
+#define INFEROP_SPLITK_WS_BYTES (32ll << 20)
+#define INFEROP_SPLITK_WS_COUNTERS 16384
+
 int inferop_hip_gemm_num_configs(void);
 int inferop_hip_gemm_config_info(int32_t cfg, inferop_gemm_cfg_info* info);
+/* Split-K workspace bytes a launch of cfg with split_k partitions needs for
+ * an m x n output (0 when it splits nothing; -1 for an invalid configuration
+ * or more output tiles than counters).  The split is clamped to k / 128 as
+ * the launch clamps it. */
+int64_t inferop_hip_gemm_workspace_bytes(int32_t cfg, int32_t split_k, int64_t m, int64_t n,
+                                         int64_t k);
 int inferop_hip_gemm_w8a8_block(void* c, const uint8_t* a_q, const float* a_scales,
                                 const uint8_t* b_q, const float* b_scales, int64_t m, int64_t n,
                                 int64_t k, int32_t out_dt, const inferop_gemm_launch* launch,

@@ -221,6 +221,20 @@ GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
   return {kPreN128M128S2, int32_t(split)};
 }
 
+// The automatic choice with its K split reduced, where needed, to what the
+// split-K workspace the library keeps per stream holds (a long K on the
+// decode kernels would otherwise ask for one partial tile per few groups).
+GemmChoice choose_gemm(int64_t m, int64_t n, int64_t k, int cus) {
+  GemmChoice ch = select_gemm(m, n, k, cus);
+  while (ch.split > 1) {
+    const int64_t b = inferop_hip_gemm_workspace_bytes(ch.cfg, ch.split, m, n, k);
+    if (b >= 0 && b <= INFEROP_SPLITK_WS_BYTES) break;
+    const int64_t s = b < 0 ? 1 : (int64_t)ch.split * INFEROP_SPLITK_WS_BYTES / b;
+    ch.split = int32_t(s < ch.split ? (s < 1 ? 1 : s) : ch.split - 1);
+  }
+  return ch;
+}
+
 // ---- implementations shared by the C++ and C entry points --------------------
 int quant_impl(void* q, void* scales, const void* x, int32_t dt, int64_t rows, int64_t cols,
                int32_t group_size, void* stream) {
@@ -337,7 +351,7 @@ int gemm_impl(void* c, const void* a_q, const void* a_scales, const void* b_q,
   if (!valid_input_dtype(out_dt)) return INFEROP_ERR_DTYPE;  // reference :185-186 silent no-op
   const DeviceEntry* d = gemm_device();
   if (!d) return INFEROP_ERR_DEVICE;
-  const GemmChoice ch = select_gemm(m, n, k, d->cus);
+  const GemmChoice ch = choose_gemm(m, n, k, d->cus);
   return gemm_launch(c, a_q, a_scales, b_q, b_scales, m, n, k, out_dt, ch.cfg, ch.split, stream);
 }
 
@@ -357,10 +371,14 @@ int gemm_impl(void* c, const void* a_q, const void* a_scales, const void* b_q,
 // 128x128 and 385 us tiled; 512 rows 592 vs 843 us tiled).  With an odd
 // K / 128 the tiled kernels: 16-row tiles below 16 rows per expert, 32-row
 // below 24, 64-row three-stage below 64, 128x128 beyond.
-int32_t select_grouped(int64_t m, int64_t k, int64_t num_experts) {
+// m: the rows the tile choice is made for (masked layout: the expected rows
+// per expert times the experts); launch_m: the rows the grid is launched over
+// (masked layout: experts * max_m), which the wide decode kernel's grid limit
+// applies to.
+int32_t select_grouped(int64_t m, int64_t launch_m, int64_t k, int64_t num_experts) {
   const int64_t avg = m / (num_experts > 0 ? num_experts : 1);
-  const int64_t ne = num_experts < m ? num_experts : m;
-  if (avg <= 8 && 16 * k <= 0x7FFFFFFF && (m + 15) / 16 + ne <= 65535) return kDwM16K4;
+  const int64_t ne = num_experts < launch_m ? num_experts : launch_m;
+  if (avg <= 8 && 16 * k <= 0x7FFFFFFF && (launch_m + 15) / 16 + ne <= 65535) return kDwM16K4;
   if ((k / 128) % 2 == 0) return avg < 96 ? kPerN128M128 : kPerN256M256;
   if (avg < 16) return kPreN128M16S4;
   if (avg < 24) return kPreN128M32S4;
@@ -415,7 +433,7 @@ int masked_impl(void* c, const void* a_q, const void* a_scales, const void* b_q,
   if (!valid_input_dtype(out_dt)) return INFEROP_ERR_DTYPE;
   if (cfg < 0) {
     const int64_t rows = expected_m > 0 ? (expected_m < max_m ? expected_m : max_m) : max_m;
-    cfg = select_grouped(rows * experts, k, experts);
+    cfg = select_grouped(rows * experts, experts * max_m, k, experts);
   }
   if (max_m == 0) return INFEROP_OK;
   if (!gemm_device()) return INFEROP_ERR_DEVICE;
@@ -432,7 +450,7 @@ int grouped_impl(void* c, const void* a_q, const void* a_scales, const void* b_q
   if (m == 0) return INFEROP_OK;
   if (!gemm_device()) return INFEROP_ERR_DEVICE;
   return grouped_launch(c, a_q, a_scales, b_q, b_scales, offsets, m, n, k, experts, 0, out_dt,
-                        select_grouped(m, k, experts), stream);
+                        select_grouped(m, m, k, experts), stream);
 }
 
 }  // namespace
@@ -603,6 +621,9 @@ extern "C" int inferop_w8a8_block_fp8_gemm_config(void* c, const void* a_q, cons
   inferop_gemm_cfg_info info{};
   if (inferop_hip_gemm_config_info(config, &info) != 0) return INFEROP_ERR_ARGUMENT;
   if (info.kind == 3 && (k / 128) % 2 != 0) return INFEROP_ERR_ARGUMENT;
+  // the split-K workspace has a fixed capacity
+  const int64_t ws = inferop_hip_gemm_workspace_bytes(config, split_k, m, n, k);
+  if (ws < 0 || ws > INFEROP_SPLITK_WS_BYTES) return INFEROP_ERR_ARGUMENT;
   if (!gemm_device()) return INFEROP_ERR_DEVICE;
   return gemm_launch(c, a_q, a_scales, b_q, b_scales, m, n, k, out_dt, config, split_k, stream);
 }
@@ -659,7 +680,18 @@ extern "C" int inferop_grouped_gemm_select(int64_t m, int64_t n, int64_t k, int6
                                            int32_t* config) {
   if (m < 0 || n <= 0 || k <= 0 || k % 128 != 0 || num_experts <= 0 || !config)
     return INFEROP_ERR_ARGUMENT;
-  *config = select_grouped(m, k, num_experts);
+  *config = select_grouped(m, m, k, num_experts);
+  return INFEROP_OK;
+}
+
+extern "C" int inferop_grouped_gemm_masked_select(int64_t max_m, int64_t n, int64_t k,
+                                                  int64_t num_experts, int64_t expected_m,
+                                                  int32_t* config) {
+  if (max_m < 0 || n <= 0 || k <= 0 || k % 128 != 0 || num_experts <= 0 || !config ||
+      (max_m > 0 && num_experts > 0x7FFFFFFF / max_m))
+    return INFEROP_ERR_ARGUMENT;
+  const int64_t rows = expected_m > 0 ? (expected_m < max_m ? expected_m : max_m) : max_m;
+  *config = select_grouped(rows * num_experts, num_experts * max_m, k, num_experts);
   return INFEROP_OK;
 }
 
@@ -667,7 +699,7 @@ extern "C" int inferop_gemm_select(int64_t m, int64_t n, int64_t k, int32_t* con
                                    int32_t* split_k) {
   if (m <= 0 || n <= 0 || k <= 0 || k % 128 != 0 || !config || !split_k) return INFEROP_ERR_ARGUMENT;
   const DeviceEntry* d = current_device();
-  const GemmChoice ch = select_gemm(m, n, k, d ? d->cus : 256);
+  const GemmChoice ch = choose_gemm(m, n, k, d ? d->cus : 256);
   *config = ch.cfg;
   *split_k = ch.split;
   return INFEROP_OK;

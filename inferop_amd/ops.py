@@ -201,6 +201,16 @@ def grouped_gemm_select(m: int, n: int, k: int, num_experts: int) -> int:
     return cfg.value
 
 
+def grouped_gemm_masked_select(max_m: int, n: int, k: int, num_experts: int,
+                               expected_m: int = 0) -> int:
+    cfg = ctypes.c_int32()
+    st = lib().inferop_grouped_gemm_masked_select(max_m, n, k, num_experts, expected_m,
+                                                  ctypes.byref(cfg))
+    if st != Status.OK:
+        raise InferopError(st, "grouped_gemm_masked_select")
+    return cfg.value
+
+
 def selftest_fp8_codec(counts, lo: int = 0, hi: int = 1 << 32, stream=None) -> int:
     return lib().inferop_selftest_fp8_codec(lo, hi, _ptr(counts), _stream(stream))
 

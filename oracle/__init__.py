@@ -194,6 +194,17 @@ def ref_quant(x: np.ndarray, group_size: int = 128):
     return q, s
 
 
+def ref_dequant(q: np.ndarray, s: np.ndarray, group_size: int = 128) -> np.ndarray:
+    """The reference's own dequantizer (reference.cpp:82-91, compiled into
+    oracle/_ref) on q [rows, cols] uint8 and s [rows, cols/gs] fp32."""
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    s = np.ascontiguousarray(s, dtype=np.float32)
+    rows, cols = q.shape
+    x = np.empty((rows, cols), np.float32)
+    ref().ref_dequant(_ptr(x, _f32p), _ptr(q, _u8p), _ptr(s, _f32p), rows, cols, group_size)
+    return x
+
+
 def ref_gemm(a_q, a_s, b_q, b_s) -> np.ndarray:
     a_q = np.ascontiguousarray(a_q, dtype=np.uint8)
     b_q = np.ascontiguousarray(b_q, dtype=np.uint8)

@@ -10,7 +10,8 @@ import torch
 import datagen
 import inferop_amd
 import oracle
-from gpu_util import assert_gemm_close, bf16_dev, device, out_to_f32, to_dev, to_np
+from gpu_util import (anchor_ref_rows, assert_gemm_close, assert_gemm_close_dev, bf16_dev, device,
+                      gemm_ref_f64, out_to_f32, to_dev, to_np)
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 DT = inferop_amd.dtype
@@ -77,7 +78,8 @@ def test_reference_gpu_cross_check(m, n, k, out, rtol, atol):
     (test_gemm.cpp:28-45), and every element within atol + rtol * |want| of the
     CPU reference (test_util.h:44-63) with the reference's tolerances.  The
     reference draws from one mt19937 stream; these are seeded numpy draws of the
-    same distributions.  The 4096^3 case checks 64 sampled rows."""
+    same distributions.  The 4096^3 case compares every element with the
+    float64 GPU reference, itself checked against the oracle on 64 rows."""
     device()
     print(f"reference cross-check {m}x{n}x{k} {out}", flush=True)
     g = datagen.rng(900 + m + k, 3)
@@ -89,15 +91,22 @@ def test_reference_gpu_cross_check(m, n, k, out, rtol, atol):
     q, s = inferop_amd.quantize(to_dev(a))
     assert np.array_equal(to_np(q), aq)
     assert np.array_equal(to_np(s).view(np.uint32), as_.view(np.uint32))
-    c = out_to_f32(_gemm(q, s, to_dev(bq), to_dev(bs), m, n, k, out=out))
-    rows = np.arange(m) if m <= 256 else np.unique(
-        np.concatenate([[0, m - 1], g.integers(0, m, 62)]))
-    want = oracle.gemm_rows(aq, as_, bq, bs, rows).astype(np.float64)
-    diff = np.abs(c[rows].astype(np.float64) - want)
-    tol = atol + rtol * np.abs(want)
+    cd = _gemm(q, s, to_dev(bq), to_dev(bs), m, n, k, out=out)
+    if m <= 256:
+        c = out_to_f32(cd)
+        want = oracle.gemm(aq, as_, bq, bs).astype(np.float64)
+        diff = np.abs(c.astype(np.float64) - want)
+        tol = atol + rtol * np.abs(want)
+    else:
+        rows = np.unique(np.concatenate([[0, m - 1], g.integers(0, m, 62)]))
+        ref = gemm_ref_f64(q, s, to_dev(bq), to_dev(bs))
+        anchor_ref_rows(ref, oracle.gemm_rows(aq, as_, bq, bs, rows), rows, "4096^3")
+        assert bool(torch.isfinite(cd).all())
+        diff = (cd.double() - ref).abs()
+        tol = atol + rtol * ref.abs()
     bad = diff > tol
-    assert not bad.any(), (f"{int(bad.sum())}/{bad.size} mismatch, "
-                           f"worst excess {float((diff - tol).max()):.4g}")
+    nbad, total = int(bad.sum()), int(np.prod(bad.shape))
+    assert nbad == 0, f"{nbad}/{total} mismatch, worst excess {float((diff - tol).max()):.4g}"
 
 
 @pytest.mark.gpu
@@ -111,11 +120,17 @@ def test_config4_ragged_stress(m):
     q, s = inferop_amd.quantize(bf16_dev(a_bits))
     aq, as_ = oracle.quant(a_f32)
     assert np.array_equal(to_np(q), aq)
-    c = out_to_f32(_gemm(q, s, to_dev(bq), to_dev(bs), m, n, k))
+    assert np.array_equal(to_np(s).view(np.uint32), as_.view(np.uint32))
+    bqd, bsd = to_dev(bq), to_dev(bs)
+    c = _gemm(q, s, bqd, bsd, m, n, k)
     rows = np.arange(m) if m <= 128 else np.unique(np.concatenate(
         [[0, m - 1, m - 2], np.random.default_rng(m).integers(0, m, 29)]))
     want = oracle.gemm_rows(aq, as_, bq, bs, rows)
-    assert_gemm_close(c[rows], want, f"config4 m={m}")
+    assert_gemm_close(out_to_f32(c)[rows], want, f"config4 m={m}")
+    # every element, against the float64 GPU reference anchored to the oracle rows
+    ref = gemm_ref_f64(q, s, bqd, bsd)
+    anchor_ref_rows(ref, want, rows, f"config4 m={m}")
+    assert_gemm_close_dev(c, ref, f"config4 m={m} all elements")
 
 
 def _device_case(m, n, k, seed):
@@ -137,19 +152,27 @@ def _device_case(m, n, k, seed):
     return a, aq, as_, bq.contiguous(), bs.contiguous()
 
 
-def _check_sampled(a, aq, as_, bq, bs, c, rows, what):
+def _check_full(a, aq, as_, bq, bs, outs, rows, what):
+    """Every element of every output in `outs` against the float64 GPU
+    reference; the reference is first checked against the oracle
+    (reference.cpp:93-110) on the sampled rows, and the GPU quantizer's bytes
+    and scales on those rows against the oracle's quantizer."""
     aq_h, as_h = to_np(aq[rows]), to_np(as_[rows])
     # the GPU quantizer's rows equal the oracle's on the same bf16 inputs
     qr, sr = oracle.quant(datagen.bf16_bits_to_f32(to_np(a[rows])))
     assert np.array_equal(aq_h, qr), what
     assert np.array_equal(as_h.view(np.uint32), sr.view(np.uint32)), what
     want = oracle.gemm_rows(aq_h, as_h, to_np(bq), to_np(bs), np.arange(len(rows)))
-    return assert_gemm_close(out_to_f32(c[rows]), want, what)
+    ref = gemm_ref_f64(aq, as_, bq, bs)
+    anchor_ref_rows(ref, want, rows, what)
+    for name, c in outs.items():
+        assert_gemm_close(out_to_f32(c[rows]), want, f"{what} {name} sampled rows")
+        assert_gemm_close_dev(c, ref, f"{what} {name} all elements")
 
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("nk", [(24576, 1536), (32768, 512), (7168, 16384), (4608, 7168)])
-def test_config2_prefill_sampled(nk):
+def test_config2_prefill_all_elements(nk):
     device()
     m = 4096
     n, k = nk
@@ -157,21 +180,20 @@ def test_config2_prefill_sampled(nk):
     a, aq, as_, bq, bs = _device_case(m, n, k, seed=200)
     c = _gemm(aq, as_, bq, bs, m, n, k)
     rows = np.unique(np.concatenate([[0, 1, 4095], np.random.default_rng(n).integers(0, m, 9)]))
-    _check_sampled(a, aq, as_, bq, bs, c, rows, f"config2 {n}x{k}")
+    _check_full(a, aq, as_, bq, bs, {"bf16": c}, rows, f"config2 {n}x{k}")
 
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("m", [128, 512, 1024, 2048, 8192])
 @pytest.mark.parametrize("nk", [(7168, 18432), (36864, 7168), (7168, 2048), (4096, 512)])
-def test_config3_m_sweep_sampled(m, nk):
+def test_config3_m_sweep_all_elements(m, nk):
     device()
     n, k = nk
     print(f"config3 m={m} n={n} k={k}", flush=True)
     a, aq, as_, bq, bs = _device_case(m, n, k, seed=300 + m)
     rows = np.unique(np.concatenate([[0, m - 1], np.random.default_rng(m + n).integers(0, m, 4)]))
-    for out in ("bf16", "fp16"):
-        c = _gemm(aq, as_, bq, bs, m, n, k, out=out)
-        _check_sampled(a, aq, as_, bq, bs, c, rows, f"config3 {m}x{n}x{k} {out}")
+    outs = {out: _gemm(aq, as_, bq, bs, m, n, k, out=out) for out in ("bf16", "fp16")}
+    _check_full(a, aq, as_, bq, bs, outs, rows, f"config3 {m}x{n}x{k}")
 
 
 N_CONFIGS = inferop_amd.gemm_num_configs()
@@ -213,7 +235,7 @@ def test_persistent_kernels_match_tiled_kernel(name):
             got = _gemm(aq, as_, bq, bs, m, n, k, out, _cfg(name), 1)
             assert torch.equal(got, want), f"{name} {m}x{n}x{k} {out}"
         rows = np.unique(np.concatenate([[0, m - 1], np.random.default_rng(m).integers(0, m, 4)]))
-        _check_sampled(a, aq, as_, bq, bs, got, rows, f"{name} {m}x{n}x{k}")
+        _check_full(a, aq, as_, bq, bs, {"fp32": got}, rows, f"{name} {m}x{n}x{k}")
 
 
 @pytest.mark.gpu

@@ -102,3 +102,59 @@ def test_graph_grouped_masked_routing_changes_between_replays():
         assert torch.equal(c, want), f"replay {rep}"
         for e in range(experts):
             assert (c[e, cnt[e]:] == -7.0).all(), f"replay {rep} expert {e}"
+
+
+def _cfg(name):
+    return next(i for i in range(inferop_amd.gemm_num_configs())
+                if inferop_amd.gemm_config_name(i) == name)
+
+
+@pytest.mark.gpu
+def test_graph_split_k_workspace_survives_larger_eager_calls():
+    # The split-K workspace of a stream has a fixed size and is never freed or
+    # replaced: a graph captured with a small split-K shape -- here the first
+    # split-K call on its stream, so the workspace is created during the
+    # capture -- must replay correctly after larger split-K shapes ran eagerly
+    # on the same stream.
+    device()
+    cfg = _cfg("pre_n128_m32_w8_s4")
+    small, large = (64, 256, 2048, 4), (64, 2112, 7168, 14)
+    cases = {}
+    for (m, n, k, split) in (small, large):
+        _, a_f32, bq, bs = datagen.gemm_case(m, n, k, seed=n)
+        aq, as_ = oracle.quant(a_f32)
+        cases[(m, n, k)] = ([to_dev(v) for v in (aq, as_, bq, bs)],
+                            oracle.gemm(aq, as_, bq, bs))
+    st = torch.cuda.Stream()
+    other = torch.cuda.Stream()
+
+    def call(shape, split, out, stream):
+        m, n, k = shape
+        args, _ = cases[shape]
+        assert inferop_amd.w8a8_block_fp8_gemm_config(out, *args, m, n, k, DT.fp32, cfg, split,
+                                                      stream.cuda_stream) == 0
+
+    s_shape, l_shape = small[:3], large[:3]
+    c_small = torch.empty(small[:2], dtype=torch.float32, device="cuda:0")
+    c_large = torch.empty(large[:2], dtype=torch.float32, device="cuda:0")
+    want_small = torch.empty_like(c_small)
+    with torch.cuda.stream(other):
+        call(s_shape, small[3], want_small, other)
+    other.synchronize()
+    assert_gemm_close(want_small.cpu().numpy(), cases[s_shape][1], "small eager")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        call(s_shape, small[3], c_small, st)
+    for rep in range(3):
+        c_large.zero_()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(st):
+            call(l_shape, large[3], c_large, st)
+        st.synchronize()
+        assert_gemm_close(c_large.cpu().numpy(), cases[l_shape][1], f"large eager {rep}")
+        c_small.zero_()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(st):
+            g.replay()
+        st.synchronize()
+        assert torch.equal(c_small, want_small), f"replay {rep}"

@@ -260,3 +260,61 @@ def test_no_cpu_fallback_symbols():
     # the product must not link the oracle
     syms = _dynamic_symbols()
     assert not any(s.startswith("orc_") or s.startswith("ref_") for s in syms)
+
+
+SPLITK_WS_BYTES = 32 << 20  # INFEROP_SPLITK_WS_BYTES (inferop_amd/csrc/hip_launch.h)
+
+
+def _tile_of(name):
+    """(bn, bm) output tile of a split-capable configuration, from its name."""
+    if name.startswith(("decl_", "dec_m16")):
+        return 16, 16
+    if name.startswith("dec_m"):
+        return 16, int(name.split("_")[1][1:])
+    bn = int(name.split("_n")[1].split("_")[0])
+    bm = int(name.split("_m")[1].split("_")[0])
+    return bn, bm
+
+
+def test_automatic_split_fits_the_fixed_workspace():
+    # the split-K workspace per stream has a fixed capacity and is never grown;
+    # the automatic choice must stay within it at every shape, including a K
+    # so long that the decode kernels would otherwise split it thousands of ways
+    names = [inferop_amd.gemm_config_name(i) for i in range(inferop_amd.gemm_num_configs())]
+    shapes = [(m, n, k) for m in (1, 8, 16, 33, 64, 65, 100, 128, 129, 300, 1000, 4096)
+              for (n, k) in ((7168, 2048), (2112, 7168), (128, 65536), (36864, 7168),
+                             (512, 1 << 20), (7168, 1 << 24), (64, 1 << 24))]
+    for (m, n, k) in shapes:
+        cfg, split = inferop_amd.gemm_select(m, n, k)
+        if split == 1 or names[cfg].startswith(("per_", "dw_")):
+            continue
+        bn, bm = _tile_of(names[cfg])
+        tiles = -(-n // bn) * -(-m // bm)
+        assert min(split, k // 128) * tiles * bn * bm * 4 <= SPLITK_WS_BYTES, (m, n, k, split)
+
+
+def test_forced_split_beyond_workspace_is_rejected():
+    # checked before any device work: a split whose partials exceed the fixed
+    # workspace is an argument error, one that fits is not rejected for it
+    S = inferop_amd.Status
+    names = [inferop_amd.gemm_config_name(i) for i in range(inferop_amd.gemm_num_configs())]
+    g = inferop_amd.w8a8_block_fp8_gemm_config
+    cfg = names.index("pre_n128_m128_w4_s2")
+    # 4096 x 4096 output = 1024 tiles of 64 KB: split 2 needs 128 MB
+    assert g(0, 0, 0, 0, 0, 4096, 4096, 4096, inferop_amd.dtype.bf16, cfg, 2) == S.ERR_ARGUMENT
+    # 256 x 256 output = 4 tiles: split 32 needs 8 MB (passes the check; without
+    # a device the call then stops at the device check)
+    assert g(0, 0, 0, 0, 0, 256, 256, 4096, inferop_amd.dtype.bf16, cfg, 32) != S.ERR_ARGUMENT
+
+
+def test_masked_selection_checks_the_launch_grid():
+    # the wide decode kernel's grid holds ceil(E * max_m / 16) + E rows of
+    # workgroups (at most 65535): a small expected_m must not pick it when the
+    # launch rows exceed that
+    names = [inferop_amd.gemm_config_name(i) for i in range(inferop_amd.gemm_num_configs())]
+    sel = lambda max_m, e, exp: names[inferop_amd.grouped_gemm_masked_select(max_m, 4096, 7168,
+                                                                             e, exp)]
+    assert sel(64, 32, 4) == "dw_m16_k4_w3a3"
+    assert sel(4096, 256, 4) != "dw_m16_k4_w3a3"
+    assert sel(4096, 256, 4).startswith("per_")
+    assert sel(1024, 64, 8) == "dw_m16_k4_w3a3"  # 4096 + 64 rows of workgroups

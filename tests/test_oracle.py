@@ -402,3 +402,50 @@ def test_topk_softmax_closed_form():
         _, w0 = oracle.topk_softmax(lg, k, False)
         l = np.exp(lg.astype(np.float64) - lg.max(axis=1, keepdims=True)).sum(axis=1, keepdims=True)
         assert np.allclose(w0, np.sort(p / l, axis=1)[:, ::-1][:, :k], rtol=1e-5, atol=1e-9)
+
+
+def _dequant_cases(gs):
+    """(q, s) pairs: seeded quantizer outputs of normal and stress activations,
+    every byte value (NaN codes 0x7F/0xFF included) under scales spanning the
+    fp32 range (subnormal, 1, huge enough to overflow), and the quantizer's
+    edge groups (zeros, Inf/NaN, denormal inputs)."""
+    out = []
+    for dist in ("normal", "stress"):
+        x = datagen.activations(24, 10 * gs, 31 + gs, dist)
+        out.append(oracle.quant(x, gs))
+    g = np.random.default_rng(gs)
+    q = np.tile(np.arange(256, dtype=np.uint8), (6, (2 * gs + 255) // 256))[:, :2 * gs]
+    q = np.ascontiguousarray(np.concatenate([q, g.integers(0, 256, (6, 2 * gs), dtype=np.uint8)],
+                                            axis=1))
+    s = np.array([[1.0, 2.0 ** -149, 3.5e-39, 0.0123, 1e30, 3.4e38, 7.0, -0.5][i % 8]
+                  for i in range(6 * 4)], np.float32).reshape(6, 4)
+    out.append((q, s))
+    if gs == 128:
+        for kind in ("bf16", "fp16", "fp32"):
+            out.append(oracle.quant(datagen.special_groups(kind)))
+    return out
+
+
+@needs_ref
+@pytest.mark.parametrize("gs", [128, 64, 48, 40])
+def test_dequant_matches_reference(gs):
+    # reference.cpp:82-91: x = e4m3_to_float(q) * scale, an fp32 product
+    for q, s in _dequant_cases(gs):
+        got = oracle.dequant(q, s, gs)
+        want = oracle.ref_dequant(q, s, gs)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("gs", [128, 64, 48, 40])
+def test_dequant_closed_form(gs):
+    # the same cases against the closed form: the E4M3 value (the 256-entry
+    # table pinned by the OCP definition) times its group's scale, rounded to
+    # fp32 by numpy; NaN codes give NaN (compared as NaN)
+    table = oracle.e4m3_decode_table()
+    for q, s in _dequant_cases(gs):
+        with np.errstate(over="ignore", invalid="ignore"):
+            want = table[q] * np.repeat(s, gs, axis=1)
+        got = oracle.dequant(q, s, gs)
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(got), nan)
+        assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
