@@ -60,6 +60,25 @@ int inferop_w8a8_block_fp8_gemm(void* c, const void* a_q, const void* a_scales, 
                                 int32_t group_size, int32_t block_n, int32_t out_dt,
                                 void* stream);
 
+/* --- allocation-free variant of inferop_w8a8_block_fp8_gemm ---
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.  Same arguments, guards, kernel choice and results as
+ * inferop_w8a8_block_fp8_gemm; the split-K partials and counters live in a
+ * fixed device array of 32 MiB + 64 KiB per GPU (held from library load until
+ * the process ends; its address is looked up on the first call on a device)
+ * instead of a per-stream workspace, so no call allocates.  Limit: a shape
+ * whose automatic choice needs more split-K scratch than that array returns
+ * INFEROP_ERR_ARGUMENT and writes nothing (no shape does: the automatic
+ * choice stays within the same capacity).  Every split-K call on one GPU
+ * shares the array: such calls that overlap in time on one GPU (other
+ * streams, a graph replayed beside eager calls) race and must not be issued;
+ * the counters return to zero at the end of every call. */
+int inferop_w8a8_block_fp8_gemm_noalloc(void* c, const void* a_q, const void* a_scales,
+                                        const void* b_q, const void* b_scales, int64_t m,
+                                        int64_t n, int64_t k, int32_t group_size,
+                                        int32_t block_n, int32_t out_dt, void* stream);
+
 /* --- replaces ops.h:108-110 topk_softmax ---
  * tokens <= 0, num_experts <= 0, num_experts > 1024, topk <= 0 or
  * topk > num_experts return INFEROP_ERR_SHAPE and write nothing (the

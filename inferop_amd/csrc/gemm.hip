@@ -1539,6 +1539,58 @@ hipError_t get_workspace(hipStream_t st, float** ws, int** cnt) {
   return hipSuccess;
 }
 
+// ---- scratch of the allocation-free entry point --------------------------------
+// inferop_hip_gemm_w8a8_block_noalloc takes its split-K partials and counters
+// from this file-scope array (one copy per GPU, held from module load until the
+// process ends) instead of the per-stream workspace, so it never allocates.
+// Same layout and capacity as a workspace: partials, then the counters.  In
+// host code `scratch` is a host-side stand-in; the device address of each
+// GPU's copy comes from hipGetSymbolAddress with that device current, kept in
+// g_scratch_ptr, and only that address is ever passed to a kernel.
+constexpr size_t kScratchBytes =
+    (size_t)INFEROP_SPLITK_WS_BYTES + (size_t)INFEROP_SPLITK_WS_COUNTERS * 4;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+std::once_flag g_scratch_once[64];
+hipError_t g_scratch_err[64];
+char* g_scratch_ptr[64];
+
+// The current device's scratch address, looked up on the first call on that
+// device (which also zeroes the counters on that call's stream, ahead of its
+// GEMM; afterwards every launch leaves them at zero).
+hipError_t get_scratch(hipStream_t st, float** ws, int** cnt) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+  std::call_once(g_scratch_once[dev], [&] {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    hipError_t r = hipStreamIsCapturing(st, &cs);
+    // under capture the symbol lookup (which may load the code object) runs in
+    // relaxed capture mode; the zeroing kernel becomes part of the graph
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    const bool capturing = r == hipSuccess && cs != hipStreamCaptureStatusNone;
+    if (capturing) r = hipThreadExchangeStreamCaptureMode(&mode);
+    void* ptr = nullptr;
+    if (r == hipSuccess) r = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (capturing) {
+      const hipError_t r2 = hipThreadExchangeStreamCaptureMode(&mode);
+      if (r == hipSuccess) r = r2;
+    }
+    if (r == hipSuccess && ptr == nullptr) r = hipErrorInvalidSymbol;
+    if (r == hipSuccess) {
+      g_scratch_ptr[dev] = static_cast<char*>(ptr);
+      r = launch_fill_zero(reinterpret_cast<int*>(g_scratch_ptr[dev] + INFEROP_SPLITK_WS_BYTES),
+                           INFEROP_SPLITK_WS_COUNTERS, st);
+    }
+    g_scratch_err[dev] = r;
+  });
+  if (g_scratch_err[dev] != hipSuccess) return g_scratch_err[dev];
+  *ws = reinterpret_cast<float*>(g_scratch_ptr[dev]);
+  *cnt = reinterpret_cast<int*>(g_scratch_ptr[dev] + INFEROP_SPLITK_WS_BYTES);
+  return hipSuccess;
+}
+
 // Workspace a launch of configuration cf with `split` K partitions needs
 // (0 without a split), and whether it fits the fixed capacity.
 int64_t workspace_bytes(const CfgEntry& cf, int64_t split, int64_t m, int64_t n) {
@@ -1613,9 +1665,15 @@ extern "C" int64_t inferop_hip_gemm_workspace_bytes(int32_t cfg, int32_t split, 
 
 namespace inferop_hip {
 namespace {
+// Split-K partials and counters for a launch: the stream's workspace, or with
+// noalloc the file-scope scratch.
+hipError_t splitk_buffers(bool noalloc, hipStream_t st, float** ws, int** cnt) {
+  return noalloc ? get_scratch(st, ws, cnt) : get_workspace(st, ws, cnt);
+}
+
 int gemm_block(void* c, const uint8_t* a_q, const float* a_scales, const uint8_t* b_q,
                const float* b_scales, int64_t m, int64_t n, int64_t k, int32_t out_dt,
-               const inferop_gemm_launch* launch, void* stream) {
+               const inferop_gemm_launch* launch, void* stream, bool noalloc) {
   const int di = dt_index(out_dt);
   if (di < 0 || !launch || launch->cfg < 0 || launch->cfg >= kNumCfgs) return hipErrorInvalidValue;
   if (m <= 0 || n <= 0 || k <= 0 || k % 128 != 0) return hipErrorInvalidValue;
@@ -1637,7 +1695,7 @@ int gemm_block(void* c, const uint8_t* a_q, const float* a_scales, const uint8_t
     if (tn > 0x7FFFFFFF || split > 65535 || tm > 65535) return hipErrorInvalidConfiguration;
     if (!workspace_fits(cf, split, m, n)) return hipErrorInvalidValue;
     if (split > 1) {
-      hipError_t e = get_workspace(st, &args.ws, &args.counters);
+      hipError_t e = splitk_buffers(noalloc, st, &args.ws, &args.counters);
       if (e != hipSuccess) return e;
     }
     hipLaunchKernelGGL(cf.fn[di], dim3((unsigned)tn, (unsigned)split, (unsigned)tm),
@@ -1673,7 +1731,7 @@ int gemm_block(void* c, const uint8_t* a_q, const float* a_scales, const uint8_t
     if ((int64_t)(cf.bn > cf.bm ? cf.bn : cf.bm) * k > 0x7FFFFFFF) return hipErrorInvalidValue;
     if (!workspace_fits(cf, split, m, n)) return hipErrorInvalidValue;
     if (split > 1) {
-      hipError_t e = get_workspace(st, &args.ws, &args.counters);
+      hipError_t e = splitk_buffers(noalloc, st, &args.ws, &args.counters);
       if (e != hipSuccess) return e;
     }
     hipLaunchKernelGGL(cf.fn[di], dim3((unsigned)tiles, (unsigned)split), dim3(64 * cf.waves), 0,
@@ -1688,7 +1746,16 @@ extern "C" int inferop_hip_gemm_w8a8_block(void* c, const uint8_t* a_q, const fl
                                            const uint8_t* b_q, const float* b_scales, int64_t m,
                                            int64_t n, int64_t k, int32_t out_dt,
                                            const inferop_gemm_launch* launch, void* stream) {
-  return gemm_block(c, a_q, a_scales, b_q, b_scales, m, n, k, out_dt, launch, stream);
+  return gemm_block(c, a_q, a_scales, b_q, b_scales, m, n, k, out_dt, launch, stream, false);
+}
+
+extern "C" int inferop_hip_gemm_w8a8_block_noalloc(void* c, const uint8_t* a_q,
+                                                   const float* a_scales, const uint8_t* b_q,
+                                                   const float* b_scales, int64_t m, int64_t n,
+                                                   int64_t k, int32_t out_dt,
+                                                   const inferop_gemm_launch* launch,
+                                                   void* stream) {
+  return gemm_block(c, a_q, a_scales, b_q, b_scales, m, n, k, out_dt, launch, stream, true);
 }
 
 extern "C" int inferop_hip_gemm_w8a8_block_grouped(void* c, const uint8_t* a_q,

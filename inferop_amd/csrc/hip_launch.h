@@ -83,6 +83,16 @@ int inferop_hip_gemm_w8a8_block(void* c, const uint8_t* a_q, const float* a_scal
                                 int64_t k, int32_t out_dt, const inferop_gemm_launch* launch,
                                 void* stream);
 
+/* Same launch without any allocation: split-K partials and counters come
+ * from a file-scope device array of INFEROP_SPLITK_WS_BYTES +
+ * 4 * INFEROP_SPLITK_WS_COUNTERS bytes per GPU (its address looked up with
+ * hipGetSymbolAddress on the first call on a device, which also zeroes the
+ * counters on that call's stream).  Calls on one GPU share it. */
+int inferop_hip_gemm_w8a8_block_noalloc(void* c, const uint8_t* a_q, const float* a_scales,
+                                        const uint8_t* b_q, const float* b_scales, int64_t m,
+                                        int64_t n, int64_t k, int32_t out_dt,
+                                        const inferop_gemm_launch* launch, void* stream);
+
 /* Grouped (MoE expert) GEMM; B [experts, n, k], b_scales [experts,
  * ceil(n/128), k/128]; C [m, n]; cfg must be a tiled configuration with a
  * grouped variant (inferop_gemm_cfg_info.grouped).

@@ -575,6 +575,33 @@ extern "C" int inferop_w8a8_block_fp8_gemm(void* c, const void* a_q, const void*
   return gemm_impl(c, a_q, a_scales, b_q, b_scales, m, n, k, group_size, block_n, out_dt, stream);
 }
 
+extern "C" int inferop_w8a8_block_fp8_gemm_noalloc(void* c, const void* a_q, const void* a_scales,
+                                                   const void* b_q, const void* b_scales,
+                                                   int64_t m, int64_t n, int64_t k,
+                                                   int32_t group_size, int32_t block_n,
+                                                   int32_t out_dt, void* stream) {
+  // gemm_impl's guards and automatic choice; only the split-K buffers differ
+  if (!gemm_shape_ok(m, n, k, group_size, block_n)) return INFEROP_ERR_SHAPE;
+  if (!valid_input_dtype(out_dt)) return INFEROP_ERR_DTYPE;
+  const DeviceEntry* d = gemm_device();
+  if (!d) return INFEROP_ERR_DEVICE;
+  const GemmChoice ch = choose_gemm(m, n, k, d->cus);
+  const int64_t need = inferop_hip_gemm_workspace_bytes(ch.cfg, ch.split, m, n, k);
+  if (need < 0 || need > INFEROP_SPLITK_WS_BYTES) {
+    std::fprintf(stderr,
+                 "[inferop] w8a8_block_fp8_gemm_noalloc: shape (m=%lld n=%lld k=%lld) needs "
+                 "%lld bytes of split-K scratch, more than the fixed %lld\n",
+                 (long long)m, (long long)n, (long long)k, (long long)need,
+                 (long long)INFEROP_SPLITK_WS_BYTES);
+    return INFEROP_ERR_ARGUMENT;
+  }
+  inferop_gemm_launch l{ch.cfg, ch.split};
+  return status_of_hip(inferop_hip_gemm_w8a8_block_noalloc(
+      c, static_cast<const uint8_t*>(a_q), static_cast<const float*>(a_scales),
+      static_cast<const uint8_t*>(b_q), static_cast<const float*>(b_scales), m, n, k, out_dt, &l,
+      stream));
+}
+
 extern "C" int inferop_topk_softmax(int32_t* topk_ids, void* topk_weights, const void* logits,
                                     int32_t tokens, int32_t num_experts, int32_t topk,
                                     int32_t renormalize, void* stream) {

@@ -105,6 +105,17 @@ def w8a8_block_fp8_gemm(c, a_q, a_scales, b_q, b_scales, m: int, n: int, k: int,
 
 
 # ---- MoE routing (reference ops.h:102-110) ---------------------------------------
+def w8a8_block_fp8_gemm_noalloc(c, a_q, a_scales, b_q, b_scales, m: int, n: int, k: int,
+                                group_size: int = 128, block_n: int = 128, out_dt=dtype.bf16,
+                                stream=None) -> int:
+    """w8a8_block_fp8_gemm without any device allocation (split-K scratch in
+    a fixed per-GPU array; no reference counterpart, for callers that cannot
+    allocate).  Split-K calls that overlap in time on one GPU race."""
+    return lib().inferop_w8a8_block_fp8_gemm_noalloc(
+        _ptr(c), _ptr(a_q), _ptr(a_scales), _ptr(b_q), _ptr(b_scales), m, n, k, group_size,
+        block_n, int(out_dt), _stream(stream))
+
+
 def topk_softmax(topk_ids, topk_weights, logits, tokens: int, num_experts: int, topk: int,
                  renormalize: bool = True, stream=None) -> int:
     return lib().inferop_topk_softmax(_ptr(topk_ids), _ptr(topk_weights), _ptr(logits), tokens,
