@@ -43,6 +43,15 @@ DECODE_M = (1, 16, 64)
 DECODE_NK = ((7168, 2048), (4096, 7168), (2112, 7168))
 PREFILL_NK = ((24576, 1536), (32768, 512), (7168, 16384), (4608, 7168))
 QUANT_SHAPES = ((4096, 7168), (4096, 16384), (8192, 18432))
+# BASELINE configs[3] (M sweep on DeepSeek-V3-like dense shapes), configs[4]
+# (ragged M, N = 4608 + 64) and the reference's own bench shape 4096^3
+# (bench/bench_kernels.cpp:63-80): timed shape by shape, bf16 output
+SWEEP_M = (128, 512, 1024, 2048, 8192)
+SWEEP_NK = ((7168, 18432), (36864, 7168), (7168, 2048), (4096, 512))
+RAGGED = ((1000, 4672, 7168), (77, 4672, 7168))
+REF_BENCH = ((4096, 4096, 4096),)
+# workgroups per CU tried for the plain-read ceiling of a decode weight stream
+READ_BLOCKS_PER_CU = (1, 2, 4, 8)
 PER_KERNEL_LAUNCHES = 20
 # prefill GEMMs per captured graph: back-to-back launches in steady state (with
 # a handful per graph the replay boundaries add tens of microseconds a launch)
@@ -266,6 +275,34 @@ def main():
         time_graphs(step_graphs, args.warmup)
         ms_step_graph = time_graphs(step_graphs, args.steps)
 
+        # The read ceiling of each decode weight stream: the library's plain
+        # read kernel over the same weight copies, launched as the GEMM is (a
+        # graph of PER_KERNEL_LAUNCHES back-to-back launches), at the best of
+        # a few grid sizes; and the launch floor (a 16-byte read).
+        cus = torch.cuda.get_device_properties(dev).multi_processor_count
+        sink = torch.zeros(4, dtype=torch.int32, device=dev)
+
+        def read_call(src, nbytes, blocks):
+            st = ia.diag_read_stream(src, nbytes, blocks, sink, sp)
+            assert st == 0, st
+
+        ceiling = {}
+        for (n, k) in DECODE_NK:
+            best = None
+            for bpc in READ_BLOCKS_PER_CU:
+                gr = capture(lambda: [read_call(W[(n, k)][r % R][0], n * k, bpc * cus)
+                                      for r in range(PER_KERNEL_LAUNCHES)])
+                time_graphs([gr], 4)
+                t = time_graphs([gr], 10) / PER_KERNEL_LAUNCHES
+                if best is None or t < best[0]:
+                    best = (t, bpc)
+                del gr
+            ceiling[(n, k)] = best
+        gl = capture(lambda: [read_call(sink, 16, 1) for _ in range(PER_KERNEL_LAUNCHES)])
+        time_graphs([gl], 4)
+        launch_floor_us = time_graphs([gl], 10) / PER_KERNEL_LAUNCHES * 1e3
+        del gl
+
         # per-kernel: a graph of PER_KERNEL_LAUNCHES back-to-back launches
         detail = []
         g_bytes = g_ms = q_bytes = q_ms = 0.0
@@ -281,10 +318,15 @@ def main():
             q_bytes += qb
             q_ms += qms
             cfg, split = ia.gemm_select(m, n, k)
+            rms, rbpc = ceiling[(n, k)]
             detail.append({"m": m, "n": n, "k": k, "gemm_us": round(gms * 1e3, 2),
                            "gemm_gbs": round(gb / (gms * 1e-3) / 1e9, 1),
                            "quant_us": round(qms * 1e3, 2),
-                           "kernel": ia.gemm_config_name(cfg), "split_k": split})
+                           "kernel": ia.gemm_config_name(cfg), "split_k": split,
+                           "stream_read_us": round(rms * 1e3, 2),
+                           "stream_ceiling_gbs": round(n * k / (rms * 1e-3) / 1e9, 1),
+                           "stream_read_blocks_per_cu": rbpc,
+                           "gemm_frac_of_stream_ceiling": round(rms / gms, 4)})
             del gq, gg
         gemm_gbs = g_bytes / (g_ms * 1e-3) / 1e9
         result.update({
@@ -307,6 +349,14 @@ def main():
                          "algorithmic_bytes_per_step": int(g_bytes),
                          "avg_launch_us": round(g_ms / len(cases) * 1e3, 3)},
             "decode_detail": detail,
+            "decode_ceiling": {
+                "what": "stream_read_us: one plain read of the shape's N*K weight bytes "
+                        "(inferop_diag_read_stream, best of 1/2/4/8 workgroups per CU) over the "
+                        "same rotating weight copies, timed like the GEMM (graph of 20 "
+                        "launches); gemm_frac_of_stream_ceiling = stream_read_us / gemm_us",
+                "launch_floor_us": round(launch_floor_us, 2),
+                "gemm_frac_of_stream_ceiling_mean": round(
+                    sum(d["gemm_frac_of_stream_ceiling"] for d in detail) / len(detail), 4)},
             "quant_decode_gbs": round(q_bytes / (q_ms * 1e-3) / 1e9, 1),
             "gpu_clocks": gpu_clocks(),
         })
@@ -380,6 +430,72 @@ def main():
                          "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tot_flops / tot_s / 1e12 / FP8_PEAK_TFLOPS, 4)}}
         torch.cuda.empty_cache()
+
+        # ---------------- matrix-core ceiling without memory ----------------
+        # 2 workgroups of 4 waves per CU (the persistent kernel's 8 waves per
+        # CU), the MFMA inner loop from registers, with and without the four
+        # promotion FMAs per MFMA; the clock the chip holds under this load
+        # sets what any GEMM can reach
+        mres = {}
+        for promote in (False, True):
+            iters = 4096
+            flops = 2 * cus * 4 * iters * 8 * 65536
+
+            def fm(promote=promote, iters=iters):
+                st = ia.diag_mfma_loop(iters, 2 * cus, promote, sink, sp)
+                assert st == 0, st
+
+            gm_ = capture(lambda: [fm() for _ in range(4)])
+            time_graphs([gm_], 2)
+            us = time_graphs([gm_], 5) / 4 * 1e3
+            mres["with_promotion" if promote else "mfma_only"] = {
+                "us": round(us, 2), "tflops": round(flops / (us * 1e-6) / 1e12, 1),
+                "frac_of_peak": round(flops / (us * 1e-6) / 1e12 / FP8_PEAK_TFLOPS, 4)}
+            del gm_
+        result["prefill"]["mfma_loop_ceiling"] = mres
+
+        # ---------------- configs[3], configs[4] and 4096^3, shape by shape ----------------
+        sweep = []
+        for (m, n, k, tag) in ([(m, n, k, "config3") for m in SWEEP_M for (n, k) in SWEEP_NK]
+                               + [(m, n, k, "config4") for (m, n, k) in RAGGED]
+                               + [(m, n, k, "ref_bench") for (m, n, k) in REF_BENCH]):
+            gb = gemm_bytes(m, n, k)
+            flops = 2.0 * m * n * k
+            bound_tflops = min(FP8_PEAK_TFLOPS, flops / gb * HBM_PEAK_GBS / 1e3)
+            hbm_bound = bound_tflops < FP8_PEAK_TFLOPS
+            # operand copies: more than 1 GiB in rotation for HBM-bound shapes
+            ncopy = min(PREFILL_LAUNCHES, max(2, -(-(1 << 30) // gb))) if hbm_bound else 2
+            ops_ = []
+            for _ in range(ncopy):
+                q_ = rand_fp8((m, k))
+                s_ = rand_scales((m, k // 128)) * 1e3
+                ops_.append((q_, s_, rand_fp8((n, k)), rand_scales(((n + 127) // 128, k // 128)),
+                             torch.empty((m, n), dtype=torch.bfloat16, device=dev)))
+
+            def gs(i, m=m, n=n, k=k, ops_=ops_):
+                q_, s_, bq_, bs_, c_ = ops_[i % len(ops_)]
+                st = ia.w8a8_block_fp8_gemm(c_, q_, s_, bq_, bs_, m, n, k, 128, 128, DT.bf16, sp)
+                assert st == 0, st
+
+            gsw = capture(lambda: [gs(i) for i in range(PREFILL_LAUNCHES)])
+            time_graphs([gsw], 2)
+            us = time_graphs([gsw], 5) / PREFILL_LAUNCHES * 1e3
+            tflops = flops / (us * 1e-6) / 1e12
+            gbs = gb / (us * 1e-6) / 1e9
+            cfg, split = ia.gemm_select(m, n, k)
+            sweep.append({"set": tag, "m": m, "n": n, "k": k, "us": round(us, 2),
+                          "tflops": round(tflops, 1), "gbs": round(gbs, 1),
+                          "bound": "hbm" if hbm_bound else "mfma",
+                          "frac_of_roofline": round(tflops / bound_tflops, 4),
+                          "kernel": ia.gemm_config_name(cfg), "split_k": split,
+                          "operand_copies": ncopy})
+            del ops_, gsw
+            torch.cuda.empty_cache()
+        result["gemm_shapes"] = {
+            "what": "BASELINE configs[3] (M sweep), configs[4] (ragged M) and the reference "
+                    "bench's 4096^3, bf16 output, graph of 20 launches per shape; "
+                    "frac_of_roofline against min(5 PF, AI x 8 TB/s)",
+            "shapes": sweep}
 
         # ---------------- quantizer on large inputs ----------------
         qres = []
@@ -543,6 +659,7 @@ def main():
     torch.cuda.synchronize()
     if not args.no_cpu:
         result["cpu_baseline"], result["cpu_baseline_parallel"] = cpu_baseline()
+        result["cpu_baseline_prefill"] = cpu_baseline_prefill()
     print(json.dumps(result), flush=True)
 
 
@@ -562,6 +679,72 @@ def gpu_clocks():
         return None
     lines = [ln.strip() for ln in out.splitlines() if "clk" in ln.lower() and ":" in ln]
     return lines or None
+
+
+def host_cpu():
+    """The host CPU model string (/proc/cpuinfo, else lscpu) and the core
+    count the OS reports."""
+    import shutil
+    import subprocess
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.lower().startswith(("model name", "cpu model", "processor model")):
+                model = line.split(":", 1)[1].strip()
+                if model:
+                    break
+    except OSError:
+        pass
+    if not model and shutil.which("lscpu"):
+        try:
+            out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+            for line in out.splitlines():
+                if line.lower().startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+        except (OSError, subprocess.SubprocessError):
+            pass
+    return f"{model or 'unknown model'}; nproc {os.cpu_count()}"
+
+
+def cpu_baseline_prefill():
+    """The reference's CPU GEMM (reference.cpp:93-110 from oracle/_ref, else the
+    oracle's restatement), single-threaded, on two deterministic rows (0 and
+    M/2) of each configs[2] shape (M = 4096), extrapolated linearly to all M
+    rows: the naive loop's cost per row does not depend on the row."""
+    import numpy as np
+
+    import oracle
+
+    use_ref = oracle.ref_available()
+    g = np.random.default_rng(1)
+    m = 4096
+    rows = np.array([0, m // 2])
+    shapes = []
+    tot_flops = tot_s = 0.0
+    for (n, k) in PREFILL_NK:
+        aq = g.integers(0, 0x7E, (len(rows), k), dtype=np.uint8)
+        as_ = (g.random((len(rows), k // 128), dtype=np.float32) + 0.5)
+        bq = g.integers(0, 0x7E, (n, k), dtype=np.uint8)
+        bs = (g.random(((n + 127) // 128, k // 128), dtype=np.float32) * 1e-3 + 1e-4)
+        t0 = time.perf_counter()
+        if use_ref:
+            oracle.ref_gemm(aq, as_, bq, bs)
+        else:
+            oracle.gemm(aq, as_, bq, bs, threads=1)
+        dt = time.perf_counter() - t0
+        full_s = dt * m / len(rows)
+        flops = 2.0 * m * n * k
+        tot_flops += flops
+        tot_s += full_s
+        shapes.append({"n": n, "k": k, "rows_timed": len(rows), "seconds_timed": round(dt, 3),
+                       "seconds_extrapolated": round(full_s, 1),
+                       "tflops": round(flops / full_s / 1e12, 6)})
+    return {"value": round(tot_flops / tot_s / 1e12, 6), "unit": "TFLOP/s", "cores": 1,
+            "kind": "reference" if use_ref else "port",
+            "sample": f"rows 0 and 2048 of each configs[2] shape (M=4096), single thread, "
+                      f"compiled -O2, extrapolated linearly to M=4096; host CPU: {host_cpu()}",
+            "shapes": shapes}
 
 
 def cpu_baseline():
@@ -590,14 +773,7 @@ def cpu_baseline():
                 oracle.gemm(aq, as_, bq, bs, threads=1)
             t_total += time.perf_counter() - t0
             total_bytes += quant_bytes(m, k) + gemm_bytes(m, n, k)
-    cpu = "unknown"
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+    cpu = host_cpu()
     single = {"value": round(total_bytes / t_total / 1e9, 4), "unit": "GB/s", "cores": 1,
               "kind": "reference" if use_ref else "port",
               "sample": "the full decode workload once (9 quant + 9 GEMM, the GPU step's "

@@ -177,6 +177,22 @@ int inferop_w8a8_block_fp8_grouped_gemm_masked_config(void* c, const void* a_q,
  * [3] decode mismatches over the 256 bytes. */
 int inferop_selftest_fp8_codec(uint64_t lo, uint64_t hi, uint64_t* counts, void* stream);
 
+/* --- measurement kernels (no counterpart in the reference) ---
+ * The ceilings the bench holds the path's kernels against, on the current
+ * device.  inferop_diag_read_stream reads `bytes` (a multiple of 16, >= 16)
+ * from the device buffer src once with `blocks` workgroups of 256 lanes
+ * (16-byte non-temporal loads, four in flight per lane): a GEMM that streams
+ * the same bytes cannot take less time.  inferop_diag_mfma_loop runs `blocks`
+ * workgroups of 4 waves, each wave issuing iters x 8 E4M3 MFMAs of 16x16x128
+ * (65536 flops each) from registers, with promote != 0 also the four fp32
+ * scale-promotion FMAs per MFMA of the blockwise GEMM: the matrix-core rate
+ * the chip sustains without memory traffic.  sink: one device uint32 of
+ * scratch. */
+int inferop_diag_read_stream(const void* src, int64_t bytes, int32_t blocks, void* sink,
+                             void* stream);
+int inferop_diag_mfma_loop(int32_t iters, int32_t blocks, int32_t promote, void* sink,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -109,3 +109,98 @@ extern "C" int inferop_hip_selftest_fp8_codec(uint64_t lo, uint64_t hi, uint64_t
                      (unsigned long long*)counts);
   return hipGetLastError();
 }
+
+// ---- measurement kernels (bench ceilings; no counterpart in the reference) ----
+
+namespace {
+
+// A plain read of n16 16-byte words: 256 lanes per workgroup, four
+// non-temporal 16-byte loads in flight per lane (a wave reads 1 KB contiguous
+// per load instruction), grid-striding over 16 KB chunks.  The loaded words
+// feed a XOR that is stored only when it equals `magic`, so the loads cannot
+// be dropped; the store is harmless either way (sink is scratch).
+__global__ __launch_bounds__(256) void read_stream_kernel(const u32x4* __restrict__ p, int64_t n16,
+                                                          uint32_t magic, uint32_t* sink) {
+  uint32_t x = 0;
+  const int64_t stride = (int64_t)gridDim.x * 1024;
+  for (int64_t base = (int64_t)blockIdx.x * 1024; base < n16; base += stride) {
+    u32x4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t i = base + j * 256 + threadIdx.x;
+      v[j] = i < n16 ? __builtin_nontemporal_load(p + i) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+  }
+  if (x == magic) sink[0] = x;
+}
+
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+
+// The prefill GEMM's inner loop without memory: per iteration a wave issues
+// 8 independent v_mfma_scale_f32_16x16x128_f8f6f4 (E4M3 x E4M3, 65536 flops
+// each) and, with PROMOTE, the four fp32 FMAs per MFMA that apply a block
+// scale (acc = fma(partial, s, acc)).  Operands live in registers.
+template <bool PROMOTE>
+__global__ __launch_bounds__(256) void mfma_loop_kernel(int iters, uint32_t magic, uint32_t* sink) {
+  const int lane = threadIdx.x & 63;
+  i32x8_t a, b[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = 0x38383838 ^ (lane * 0x01010101 & 0x03030303);
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) b[j][i] = 0x30303030 + j + i;
+  f32x4 acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const float s = 1.0f + lane * 1e-7f;
+  for (int it = 0; it < iters; ++it) {
+    // the operands are opaque to the compiler in every iteration, so no MFMA
+    // is hoisted out of the loop (the asm emits no instruction)
+    asm volatile("" : "+v"(a));
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if constexpr (PROMOTE) {
+        const f32x4 pv = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+            a, b[j], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[j][r] = __builtin_fmaf(pv[r], s, acc[j][r]);
+      } else {
+        acc[j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b[j], acc[j], 0, 0, 0, 127,
+                                                                  0, 127);
+      }
+    }
+  }
+  float t = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) t += acc[j][0] + acc[j][1] + acc[j][2] + acc[j][3];
+  if (__builtin_bit_cast(uint32_t, t) == magic) sink[0] = magic;
+}
+
+}  // namespace
+
+extern "C" int inferop_hip_diag_read_stream(const void* src, int64_t bytes, int32_t blocks,
+                                            uint32_t* sink, void* stream) {
+  if (!src || !sink || bytes < 16 || bytes % 16 != 0 || blocks < 1 || blocks > (1 << 20))
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(read_stream_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const u32x4*>(src), bytes / 16,
+                     0x9E3779B9u, sink);
+  return hipGetLastError();
+}
+
+extern "C" int inferop_hip_diag_mfma_loop(int32_t iters, int32_t blocks, int32_t promote,
+                                          uint32_t* sink, void* stream) {
+  if (!sink || iters < 1 || blocks < 1 || blocks > (1 << 20)) return hipErrorInvalidValue;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (promote) {
+    hipLaunchKernelGGL(mfma_loop_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, st, iters,
+                       0x7F7FFFFFu, sink);
+  } else {
+    hipLaunchKernelGGL(mfma_loop_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, st, iters,
+                       0x7F7FFFFFu, sink);
+  }
+  return hipGetLastError();
+}

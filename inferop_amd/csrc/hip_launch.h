@@ -108,6 +108,17 @@ int inferop_hip_gemm_w8a8_block_grouped(void* c, const uint8_t* a_q, const float
                                         int64_t experts, int64_t max_m, int32_t out_dt,
                                         int32_t cfg, void* stream);
 
+/* ---- measurement kernels for the bench's ceilings ----
+ * read_stream: one plain read of `bytes` (a multiple of 16) from src by
+ * `blocks` workgroups of 256 lanes; sink: one device uint32 of scratch.
+ * mfma_loop: `blocks` workgroups of 4 waves, each wave issuing iters x 8
+ * E4M3 MFMAs of 16x16x128 from registers (65536 flops each), with promote the
+ * four scale-promotion FMAs per MFMA the GEMM adds. */
+int inferop_hip_diag_read_stream(const void* src, int64_t bytes, int32_t blocks, uint32_t* sink,
+                                 void* stream);
+int inferop_hip_diag_mfma_loop(int32_t iters, int32_t blocks, int32_t promote, uint32_t* sink,
+                               void* stream);
+
 /* ---- device self-test of the E4M3 conversions used by the fast paths ----
  * counts[0]: fp32 patterns in [lo, hi) inside the quantizer fast-path domain
  *            (finite, |v| < 464) where the hardware encode differs from the

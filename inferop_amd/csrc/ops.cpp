@@ -732,6 +732,23 @@ extern "C" int inferop_gemm_select(int64_t m, int64_t n, int64_t k, int32_t* con
   return INFEROP_OK;
 }
 
+extern "C" int inferop_diag_read_stream(const void* src, int64_t bytes, int32_t blocks,
+                                        void* sink, void* stream) {
+  if (!current_device()) return INFEROP_ERR_DEVICE;
+  if (!src || !sink || bytes < 16 || bytes % 16 != 0 || blocks < 1 || blocks > (1 << 20))
+    return INFEROP_ERR_ARGUMENT;
+  return status_of_hip(
+      inferop_hip_diag_read_stream(src, bytes, blocks, static_cast<uint32_t*>(sink), stream));
+}
+
+extern "C" int inferop_diag_mfma_loop(int32_t iters, int32_t blocks, int32_t promote, void* sink,
+                                      void* stream) {
+  if (!gemm_device()) return INFEROP_ERR_DEVICE;
+  if (!sink || iters < 1 || blocks < 1 || blocks > (1 << 20)) return INFEROP_ERR_ARGUMENT;
+  return status_of_hip(inferop_hip_diag_mfma_loop(iters, blocks, promote ? 1 : 0,
+                                                  static_cast<uint32_t*>(sink), stream));
+}
+
 extern "C" int inferop_selftest_fp8_codec(uint64_t lo, uint64_t hi, uint64_t* counts,
                                           void* stream) {
   if (!current_device()) return INFEROP_ERR_DEVICE;

@@ -226,6 +226,17 @@ def selftest_fp8_codec(counts, lo: int = 0, hi: int = 1 << 32, stream=None) -> i
     return lib().inferop_selftest_fp8_codec(lo, hi, _ptr(counts), _stream(stream))
 
 
+def diag_read_stream(src, nbytes: int, blocks: int, sink, stream=None) -> int:
+    """One plain read of nbytes of src (the HBM read ceiling of a stream)."""
+    return lib().inferop_diag_read_stream(_ptr(src), nbytes, blocks, _ptr(sink), _stream(stream))
+
+
+def diag_mfma_loop(iters: int, blocks: int, promote: bool, sink, stream=None) -> int:
+    """The GEMM's MFMA inner loop from registers (the matrix-core ceiling)."""
+    return lib().inferop_diag_mfma_loop(iters, blocks, 1 if promote else 0, _ptr(sink),
+                                        _stream(stream))
+
+
 # ---- tensor-level conveniences ---------------------------------------------------
 def _torch_dtype_code(t) -> dtype:
     import torch
