@@ -65,7 +65,7 @@ int inferop_w8a8_block_fp8_gemm(void* c, const void* a_q, const void* a_scales, 
  * memory: code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc.  Same arguments, guards, kernel choice and results as
  * inferop_w8a8_block_fp8_gemm; the split-K partials and counters live in a
- * fixed device array of 32 MiB + 64 KiB per GPU (held from library load until
+ * fixed device array of 64 MiB + 64 KiB per GPU (held from library load until
  * the process ends; its address is looked up on the first call on a device)
  * instead of a per-stream workspace, so no call allocates.  Limit: a shape
  * whose automatic choice needs more split-K scratch than that array returns

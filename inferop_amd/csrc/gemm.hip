@@ -72,6 +72,10 @@ struct GemmArgs {
   const int* offsets;
   int experts;
   int max_m;
+  // persistent kernels (plain GEMM): the tiles of the last, partial round are
+  // each cut into tail_split K ranges (1: whole tiles); their fp32 partials go
+  // to ws and a second kernel adds them
+  int tail_split;
 };
 
 // Raw buffer resource over `bytes` bytes at base (stride 0; dword3 selects a
@@ -1098,8 +1102,16 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_persist_kernel(GemmArgs a) 
   // grouped: the experts' M tiles, each with every N tile (N tile fastest)
   const int tiles = tiles_n * (GROUPED ? grouped_mtiles<BM>(a, lane) : tiles_m);
   const int P = gridDim.x;
+  // Work units: whole tiles, except that with a tail split S > 1 (plain GEMM)
+  // the `tail` tiles of the last, partial round (all tiles when there are
+  // fewer than P) are each cut into S K ranges of whole pairs of scale groups,
+  // one unit each (the host keeps tail * S <= P, so they run in one round).
+  const int S = (!GROUPED && a.tail_split > 1) ? a.tail_split : 1;
+  const int full = S > 1 ? tiles / P * P : tiles;
+  const int tail = tiles - full;
+  const int units = full + tail * S;
   int u = xcd_contiguous((int)blockIdx.x, P);
-  if (u >= tiles) return;
+  if (u >= units) return;
   // tile uu: first column n0, rows [m0, mend), expert e (0 when not grouped)
   auto tile_at = [&](int uu, int* n0, int* m0, int* mend, int* e) {
     if constexpr (GROUPED) {
@@ -1113,6 +1125,28 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_persist_kernel(GemmArgs a) 
       *mend = M;
       *e = 0;
     }
+  };
+
+  // unit uu: its tile (tile_at), the scale groups [gb, ge) it adds up and,
+  // for a piece of a cut tile, the piece z and the tile's tail index tt
+  // (tt = -1 for a whole tile).  Consecutive pieces are different tiles at the
+  // same K range, so an XCD's pieces share A or B rows in its L2.
+  const int NP = KG >> 1;
+  auto unit_at = [&](int uu, int* n0, int* m0, int* mend, int* e, int* gb, int* ge, int* z,
+                     int* tt) {
+    int t = uu, zz = 0, s = 1;
+    *tt = -1;
+    if (uu >= full) {
+      const int v = uu - full;
+      t = full + v % tail;
+      zz = v / tail;
+      s = S;
+      *tt = v % tail;
+    }
+    tile_at(t, n0, m0, mend, e);
+    *z = zz;
+    *gb = 2 * (int)((int64_t)zz * NP / s);
+    *ge = 2 * (int)((int64_t)(zz + 1) * NP / s);
   };
 
   const int lrow = lane >> 3;
@@ -1237,23 +1271,23 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_persist_kernel(GemmArgs a) 
       };
     };
 
-    int n0, m0, mend, ex;
-    tile_at(u, &n0, &m0, &mend, &ex);
+    int n0, m0, mend, ex, gb, ge, z, tt;
+    unit_at(u, &n0, &m0, &mend, &ex, &gb, &ge, &z, &tt);
     set_loads(n0, m0, mend, ex);
 #pragma unroll
-    for (int d = 0; d < kLoads; ++d) issue_load(0, smem0, d);
+    for (int d = 0; d < kLoads; ++d) issue_load(gb, smem0, d);
     barrier();
     for (;;) {
       const int nu = u + P;
-      const bool has_next = nu < tiles;
-      int nn0 = n0, nm0 = m0, nmend = mend, nex = ex;
-      if (has_next) tile_at(nu, &nn0, &nm0, &nmend, &nex);
+      const bool has_next = nu < units;
+      int nn0 = n0, nm0 = m0, nmend = mend, nex = ex, ngb = gb, nge = ge, nz = z, ntt = tt;
+      if (has_next) unit_at(nu, &nn0, &nm0, &nmend, &nex, &ngb, &nge, &nz, &ntt);
 #pragma unroll
       for (int i = 0; i < SN; ++i)
 #pragma unroll
         for (int j = 0; j < SM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      // on entry group 0 of the tile is in buffer 0
-      for (int g0 = 0; g0 + 2 < KG; g0 += 2) {
+      // on entry group gb of the unit is in buffer 0 (gb and ge are even)
+      for (int g0 = gb; g0 + 2 < ge; g0 += 2) {
         compute(smem0, spread(g0 + 1, smem1));
         pin_acc();
         barrier();  // group g0 + 1 landed; every wave is done with buffer 0
@@ -1261,15 +1295,28 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_persist_kernel(GemmArgs a) 
         pin_acc();
         barrier();  // group g0 + 2 landed; every wave is done with buffer 1
       }
-      compute(smem0, spread(KG - 1, smem1));
+      compute(smem0, spread(ge - 1, smem1));
       pin_acc();
-      barrier();  // group KG - 1 landed; every wave is done with buffer 0
-      // the next tile's first group (the last tile reloads its own, which
+      barrier();  // group ge - 1 landed; every wave is done with buffer 0
+      // the next unit's first group (the last unit reloads its own, which
       // keeps the group free of branches)
       set_loads(nn0, nm0, nmend, nex);
-      compute(smem1, spread(0, smem0));
+      compute(smem1, spread(ngb, smem0));
       pin_acc();
-      barrier();  // the next tile's group 0 landed; buffer 1 is free
+      barrier();  // the next unit's first group landed; buffer 1 is free
+
+      if (tt >= 0) {
+        // a piece of a cut tile (always a workgroup's last unit): its fp32
+        // partial goes to the workspace in this wave's register layout, one
+        // 1 KB store per pair; the tail kernel adds the pieces
+        const int64_t base = ((((int64_t)z * tail + tt) * NW + wave) * (SN * SM)) * 64 + lane;
+        f32x4* part = reinterpret_cast<f32x4*>(a.ws) + base;
+#pragma unroll
+        for (int i = 0; i < SN; ++i)
+#pragma unroll
+          for (int j = 0; j < SM; ++j) __builtin_nontemporal_store(acc[i][j], part + (i * SM + j) * 64);
+        break;
+      }
 
       // the output tile leaves through buffer 1, RP rows per pass
       OT* C = reinterpret_cast<OT*>(a.c);
@@ -1330,6 +1377,10 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_persist_kernel(GemmArgs a) 
       m0 = nm0;
       mend = nmend;
       ex = nex;
+      gb = ngb;
+      ge = nge;
+      z = nz;
+      tt = ntt;
     }
   };
   if (wave < NL) {
@@ -1337,6 +1388,36 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_persist_kernel(GemmArgs a) 
   } else {
     run(std::integral_constant<bool, false>{});
   }
+}
+
+// ---- tail reduction of the persistent kernel ---------------------------------------
+// One thread per (cut tile, wave, pair, lane) slot of the partial layout the
+// persistent kernel stores: the S pieces' four fp32 values are added in piece
+// order (deterministic) and the four outputs stored.  The slot's output
+// position follows the persistent kernel's wave tiling.
+template <int BN, int BM, int WN, int WM, int OUT_DT>
+__global__ __launch_bounds__(256) void gemm_tail_reduce_kernel(GemmArgs a, int full, int tail) {
+  constexpr int NW = WN * WM;
+  constexpr int TN = BN / WN, TM = BM / WM;
+  constexpr int SN = TN / 16, SM = TM / 16;
+  constexpr int kSlots = NW * SN * SM * 64;  // per tile
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (int64_t)tail * kSlots) return;
+  const int tt = (int)(t / kSlots);
+  const int r = (int)(t - (int64_t)tt * kSlots);
+  const int lane = r & 63, q = (r >> 6) % (SN * SM), wave = (r >> 6) / (SN * SM);
+  const int i = q / SM, j = q % SM, wn = wave % WN, wm = wave / WN;
+  const int tiles_n = (a.n + BN - 1) / BN, tiles_m = (a.m + BM - 1) / BM;
+  int tn, tm;
+  tile_of(full + tt, tiles_n, tiles_m, &tn, &tm);
+  const int m = tm * BM + wm * TM + 16 * j + (lane & 15);
+  const int n = tn * BN + wn * TN + 16 * i + 4 * (lane >> 4);
+  if (m >= a.m) return;
+  const f32x4* part = reinterpret_cast<const f32x4*>(a.ws) + (int64_t)tt * kSlots + r;
+  const int64_t piece = (int64_t)tail * kSlots;
+  f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int z = 0; z < a.tail_split; ++z) sum += __builtin_nontemporal_load(part + z * piece);
+  store_out4<OUT_DT>(a, m, n, sum);
 }
 
 // ---- kernel table -------------------------------------------------------------
@@ -1356,6 +1437,8 @@ struct CfgEntry {
   // scale preload, where built (else null)
   KernelFn fn_grp[3];
   KernelFn fn_grp_alt[3];
+  // persistent (kind 3): the reduction of cut tail tiles
+  void (*fn_tail[3])(GemmArgs, int, int);
 };
 
 #define DECODE_CFG(MT, WK, U, NAME)                                                           \
@@ -1424,7 +1507,12 @@ struct CfgEntry {
     gemm_persist_kernel<BN, BM, WN, WM, kBf16>},                                               \
    {gemm_persist_kernel<BN, BM, WN, WM, kFp32, true>,                                          \
     gemm_persist_kernel<BN, BM, WN, WM, kFp16, true>,                                          \
-    gemm_persist_kernel<BN, BM, WN, WM, kBf16, true>}}
+    gemm_persist_kernel<BN, BM, WN, WM, kBf16, true>},                                         \
+   {nullptr, nullptr, nullptr},                                                                \
+   {nullptr, nullptr, nullptr},                                                                \
+   {gemm_tail_reduce_kernel<BN, BM, WN, WM, kFp32>,                                            \
+    gemm_tail_reduce_kernel<BN, BM, WN, WM, kFp16>,                                            \
+    gemm_tail_reduce_kernel<BN, BM, WN, WM, kBf16>}}
 
 const CfgEntry kCfgs[] = {
     DECODE_CFG(1, 1, 8, "dec_m16_k1_u8"),
@@ -1591,6 +1679,31 @@ hipError_t get_scratch(hipStream_t st, float** ws, int** cnt) {
   return hipSuccess;
 }
 
+// Launch plan of a persistent configuration: grid, the tiles of the last,
+// partial round that are cut (tail) and into how many K ranges (split), and
+// the fp32 partial bytes they need.  The pieces of all cut tiles must run in
+// one round (tail * split <= workgroups) and each keeps a pair of groups.
+struct PersistPlan {
+  int64_t grid, tail, split, ws_bytes;
+};
+PersistPlan persist_plan(const CfgEntry& cf, int64_t tiles, int64_t kg, int64_t split, int cus) {
+  const int64_t slots = (int64_t)cus * (cf.bn * cf.bm <= 128 * 128 ? 2 : 1);
+  PersistPlan p{tiles < slots ? tiles : slots, 0, 1, 0};
+  int64_t s = split < 1 ? 1 : split;
+  if (s > kg / 2) s = kg / 2;
+  if (s <= 1) return p;
+  const int64_t tail = tiles >= slots ? tiles % slots : tiles;
+  if (tail == 0) return p;
+  const int64_t fit = slots / tail;
+  if (s > fit) s = fit;
+  if (s <= 1) return p;
+  p.tail = tail;
+  p.split = s;
+  p.grid = tiles >= slots ? slots : tiles * s;
+  p.ws_bytes = s * tail * cf.bn * cf.bm * 4;
+  return p;
+}
+
 // Workspace a launch of configuration cf with `split` K partitions needs
 // (0 without a split), and whether it fits the fixed capacity.
 int64_t workspace_bytes(const CfgEntry& cf, int64_t split, int64_t m, int64_t n) {
@@ -1658,6 +1771,12 @@ extern "C" int64_t inferop_hip_gemm_workspace_bytes(int32_t cfg, int32_t split, 
   int64_t s = split < 1 ? 1 : split;
   if (s > k / 128) s = k / 128;
   const CfgEntry& cf = kCfgs[cfg];
+  if (cf.kind == 3) {
+    int cus = 0;
+    if (device_cus(&cus) != hipSuccess) cus = 256;
+    const int64_t tiles = ((n + cf.bn - 1) / cf.bn) * ((m + cf.bm - 1) / cf.bm);
+    return persist_plan(cf, tiles, k / 128, split, cus).ws_bytes;
+  }
   const int64_t tiles = ((n + cf.bn - 1) / cf.bn) * ((m + cf.bm - 1) / cf.bm);
   if (s > 1 && cf.kind != 3 && cf.kind != 4 && tiles > INFEROP_SPLITK_WS_COUNTERS) return -1;
   return workspace_bytes(cf, s, m, n);
@@ -1711,17 +1830,31 @@ int gemm_block(void* c, const uint8_t* a_q, const float* a_scales, const uint8_t
     const KernelFn fn = per_wave <= wide_scale_cap(cf.bm / 16) ? cf.fn[di] : cf.fn_alt[di];
     hipLaunchKernelGGL(fn, dim3((unsigned)tn, (unsigned)tm), dim3(64 * cf.waves), 0, st, args);
   } else if (cf.kind == 3) {
-    // persistent: whole tiles (split_k is ignored), an even number of scale
-    // groups, one workgroup per CU (two for 128x128 tiles, whose LDS allows it)
+    // persistent: an even number of scale groups, one workgroup per CU (two
+    // for 128x128 tiles, whose LDS allows it); split_k > 1 cuts the tiles of
+    // the last, partial round into that many K ranges (fewer if the pieces
+    // would not all run at once), added by the tail kernel afterwards
     const int64_t tiles = tn * tm;
     if (tiles > 0x7FFFFFFF || kg % 2 != 0) return hipErrorInvalidValue;
     if ((int64_t)(cf.bn > cf.bm ? cf.bn : cf.bm) * k > 0x7FFFFFFF) return hipErrorInvalidValue;
     int cus = 0;
     hipError_t e = device_cus(&cus);
     if (e != hipSuccess) return e;
-    const int64_t slots = (int64_t)cus * (cf.bn * cf.bm <= 128 * 128 ? 2 : 1);
-    const int64_t grid = tiles < slots ? tiles : slots;
-    hipLaunchKernelGGL(cf.fn[di], dim3((unsigned)grid), dim3(64 * cf.waves), 0, st, args);
+    const PersistPlan pl = persist_plan(cf, tiles, kg, launch->split_k, cus);
+    if (pl.split > 1) {
+      if (pl.ws_bytes > (int64_t)INFEROP_SPLITK_WS_BYTES) return hipErrorInvalidValue;
+      e = splitk_buffers(noalloc, st, &args.ws, &args.counters);
+      if (e != hipSuccess) return e;
+    }
+    args.tail_split = pl.split;
+    hipLaunchKernelGGL(cf.fn[di], dim3((unsigned)pl.grid), dim3(64 * cf.waves), 0, st, args);
+    if (pl.split > 1) {
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      const int64_t threads = pl.tail * (int64_t)cf.bn * cf.bm / 4;
+      hipLaunchKernelGGL(cf.fn_tail[di], dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                         st, args, (int)(tiles - pl.tail), (int)pl.tail);
+    }
   } else {
     const int64_t tiles = tn * tm;
     int split = launch->split_k < 1 ? 1 : launch->split_k;

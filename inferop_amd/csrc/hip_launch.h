@@ -57,7 +57,8 @@ typedef struct {
   int32_t bm;     /* block tile along M */
   int32_t waves;  /* waves per workgroup */
   int32_t kind;   /* 1 = decode (16-row weight stripes), 2 = LDS-staged output tiles,
-                     3 = persistent LDS-staged tiles (split_k ignored, K/128 even),
+                     3 = persistent LDS-staged tiles (K/128 even; split_k > 1 cuts
+                         the tiles of the last, partial round along K),
                      4 = wide decode: a weight stripe over all of K with bm activation
                          rows (split_k ignored) */
   const char* name;
@@ -67,7 +68,7 @@ typedef struct {
 /* Capacity of the split-K workspace the library keeps per (device, stream):
  * fp32 partial bytes and arrival counters (one per output tile).  A launch
  * whose split needs more is rejected with hipErrorInvalidValue. */
-#define INFEROP_SPLITK_WS_BYTES (32ll << 20)
+#define INFEROP_SPLITK_WS_BYTES (64ll << 20)
 #define INFEROP_SPLITK_WS_COUNTERS 16384
 
 int inferop_hip_gemm_num_configs(void);

@@ -239,6 +239,31 @@ def test_persistent_kernels_match_tiled_kernel(name):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("name", ["per_n256_m256_w8", "per_n256_m128_w8", "per_n128_m128_w4"])
+def test_persistent_tail_split(name):
+    # split_k > 1 on a persistent configuration cuts the tiles of the last,
+    # partial round into K ranges whose fp32 partials a second kernel adds in
+    # piece order: every element within tolerance of the float64 reference,
+    # and bit-identical from run to run.  Shapes: a partial last round after
+    # full ones (4096 x 9216: 16 x 36 tiles of 256), fewer tiles than
+    # workgroups, ragged M and N, and a split that leaves one pair of groups
+    # per piece.
+    device()
+    for (m, n, k, split) in [(4096, 9216, 1024, 4), (700, 4100, 1536, 3), (333, 1000, 512, 2),
+                             (512, 4608, 7168, 8)]:
+        print(f"{name} tail split {split} {m}x{n}x{k}", flush=True)
+        a, aq, as_, bq, bs = _device_case(m, n, k, seed=m + n + split)
+        outs = {}
+        for out in ("bf16", "fp32"):
+            c = _gemm(aq, as_, bq, bs, m, n, k, out, _cfg(name), split)
+            again = _gemm(aq, as_, bq, bs, m, n, k, out, _cfg(name), split)
+            assert torch.equal(c, again), f"{name} {m}x{n}x{k} {out}: not repeatable"
+            outs[out] = c
+        rows = np.unique(np.concatenate([[0, m - 1], np.random.default_rng(m).integers(0, m, 4)]))
+        _check_full(a, aq, as_, bq, bs, outs, rows, f"{name} tail {split} {m}x{n}x{k}")
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("name", ["dw_m64_k4_w2a2", "dw_m64_k2_w4a2", "dw_m32_k4_w2a2",
                                   "dw_m16_k2_w8a8", "dw_m16_k8_w3a3", "dw_m16_k4_w3a3",
                                   "dw_m16_k8_w2a2"])
