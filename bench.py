@@ -438,8 +438,8 @@ def main():
         # sets what any GEMM can reach
         mres = {}
         for promote in (False, True):
-            iters = 4096
-            flops = 2 * cus * 4 * iters * 8 * 65536
+            iters = 1024
+            flops = 2 * cus * 4 * iters * 32 * 65536
 
             def fm(promote=promote, iters=iters):
                 st = ia.diag_mfma_loop(iters, 2 * cus, promote, sink, sp)

@@ -183,8 +183,9 @@ int inferop_selftest_fp8_codec(uint64_t lo, uint64_t hi, uint64_t* counts, void*
  * from the device buffer src once with `blocks` workgroups of 256 lanes
  * (16-byte non-temporal loads, four in flight per lane): a GEMM that streams
  * the same bytes cannot take less time.  inferop_diag_mfma_loop runs `blocks`
- * workgroups of 4 waves, each wave issuing iters x 8 E4M3 MFMAs of 16x16x128
- * (65536 flops each) from registers, with promote != 0 also the four fp32
+ * workgroups of 4 waves, each wave issuing iters x 32 E4M3 MFMAs of 16x16x128
+ * (65536 flops each; one wave's share of a 256x256 tile per scale group) from
+ * registers, with promote != 0 also the four fp32
  * scale-promotion FMAs per MFMA of the blockwise GEMM: the matrix-core rate
  * the chip sustains without memory traffic.  sink: one device uint32 of
  * scratch. */

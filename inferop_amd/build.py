@@ -33,7 +33,8 @@ HIP_FLAGS = [
 # per-source extra flags: MFMA results in VGPRs (not AGPRs), so the fp32
 # scale promotion reads them directly and independent MFMAs get distinct
 # destination registers
-EXTRA_FLAGS = {"gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+EXTRA_FLAGS = {"gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+               "device.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 CXX_FLAGS = ["-O2", "-fPIC", "-std=c++17", "-I" + INCLUDE, "-I" + CSRC, "-Wall", "-Wextra"]
 
 

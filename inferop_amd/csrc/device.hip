@@ -138,44 +138,60 @@ __global__ __launch_bounds__(256) void read_stream_kernel(const u32x4* __restric
 
 typedef int i32x8_t __attribute__((ext_vector_type(8)));
 
-// The prefill GEMM's inner loop without memory: per iteration a wave issues
-// 8 independent v_mfma_scale_f32_16x16x128_f8f6f4 (E4M3 x E4M3, 65536 flops
-// each) and, with PROMOTE, the four fp32 FMAs per MFMA that apply a block
-// scale (acc = fma(partial, s, acc)).  Operands live in registers.
+// The prefill GEMM's inner loop without memory, shaped as one wave's share of
+// a 256x256 tile per scale group: 8 weight slices x 4 activation slices, 32
+// v_mfma_scale_f32_16x16x128_f8f6f4 (E4M3 x E4M3, 65536 flops each) per
+// iteration; with PROMOTE each MFMA starts from zero and its four results are
+// added to fp32 accumulators with the block scale (acc = fma(partial, s, acc),
+// the GEMM's promotion), otherwise the MFMA accumulates in place.  Operands
+// live in registers and are opaque to the compiler in every iteration (the
+// asm statements emit no instruction), so nothing is hoisted out of the loop.
 template <bool PROMOTE>
 __global__ __launch_bounds__(256) void mfma_loop_kernel(int iters, uint32_t magic, uint32_t* sink) {
   const int lane = threadIdx.x & 63;
-  i32x8_t a, b[8];
+  i32x8_t w[8], x[4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) a[i] = 0x38383838 ^ (lane * 0x01010101 & 0x03030303);
+  for (int t = 0; t < 8; ++t)
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
+    for (int e = 0; e < 8; ++e) w[t][e] = 0x38383838 ^ ((lane + t + e) & 0x03030303);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) b[j][i] = 0x30303030 + j + i;
-  f32x4 acc[8];
+  for (int t = 0; t < 4; ++t)
 #pragma unroll
-  for (int j = 0; j < 8; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const float s = 1.0f + lane * 1e-7f;
+    for (int e = 0; e < 8; ++e) x[t][e] = 0x30303030 + t + e;
+  f32x4 acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float sc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) sc[j] = 1.0f + (lane + j) * 1e-7f;
   for (int it = 0; it < iters; ++it) {
-    // the operands are opaque to the compiler in every iteration, so no MFMA
-    // is hoisted out of the loop (the asm emits no instruction)
-    asm volatile("" : "+v"(a));
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if constexpr (PROMOTE) {
-        const f32x4 pv = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-            a, b[j], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
+    for (int t = 0; t < 8; ++t) asm volatile("" : "+v"(w[t]));
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[j][r] = __builtin_fmaf(pv[r], s, acc[j][r]);
-      } else {
-        acc[j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b[j], acc[j], 0, 0, 0, 127,
-                                                                  0, 127);
+    for (int t = 0; t < 4; ++t) asm volatile("" : "+v"(x[t]));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (PROMOTE) {
+          const f32x4 pv = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              w[i], x[j], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127, 0, 127);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[i][j][r] = __builtin_fmaf(pv[r], sc[j], acc[i][j][r]);
+        } else {
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w[i], x[j], acc[i][j], 0, 0,
+                                                                       0, 127, 0, 127);
+        }
       }
     }
   }
   float t = 0.f;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) t += acc[j][0] + acc[j][1] + acc[j][2] + acc[j][3];
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) t += acc[i][j][0] + acc[i][j][1] + acc[i][j][2] + acc[i][j][3];
   if (__builtin_bit_cast(uint32_t, t) == magic) sink[0] = magic;
 }
 

@@ -516,9 +516,18 @@ __host__ __device__ constexpr int wide_scale_cap(int) { return 16; }
 // Grouped mode (GROUPED): grid y enumerates virtual M tiles of 16*MT rows as in
 // the tiled kernel's grouped mode (grouped_tile); a workgroup streams one
 // 16-row stripe of its expert's weights against that expert's rows.
-template <int MT, int WK, int UW, int UA, bool PRE, int OUT_DT, bool GROUPED = false>
+//
+// NT > 1: a workgroup owns NT adjacent stripes (16 * NT weight rows inside one
+// 128-row weight block) and every wave multiplies each activation slice with
+// all NT weight slices, so a CU reads the activations once per 16 * NT weight
+// rows instead of once per 16.  With fewer stripes than CUs left, the K range
+// is split across workgroups (grid z) and the partials meet in the split-K
+// fixup.
+template <int MT, int WK, int UW, int UA, bool PRE, int OUT_DT, bool GROUPED = false, int NT = 1>
 __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
-  constexpr int kW = 2048;                            // 16 weight rows x 128 B
+  static_assert(NT == 1 || NT == 2 || NT == 4 || NT == 8, "stripes inside one weight block");
+  static_assert(NT == 1 || !GROUPED, "grouped mode streams one stripe");
+  constexpr int kW = NT * 2048;                       // 16 * NT weight rows x 128 B
   constexpr int kCap = wide_scale_cap(MT);
   constexpr int kOffSa = MT * 2048;                   // in an activation slot (no PRE)
   constexpr int kOffSb = kOffSa + 256;
@@ -526,10 +535,13 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
   constexpr int kSaF = PRE ? 16 * MT * kCap : 0;      // preloaded sa floats, [row][group]
   constexpr int kScale = PRE ? kSaF * 4 + 256 : 0;    // + up to 64 sb floats
   constexpr int kWave = UW * kW + UA * kA + kScale;
-  constexpr int kPerIter = 2 + 2 * MT + (PRE ? 0 : 2);  // loads issued per group
+  constexpr int kPerIter = 2 * NT + 2 * MT + (PRE ? 0 : 2);  // loads issued per group
+  constexpr int kPairs = NT * MT;                     // 16x16 output blocks
+  constexpr int kLP = (kPairs + WK - 1) / WK;         // blocks per wave at the end
   constexpr int kWait = (UA - 1) * kPerIter;          // loads that may stay in flight
   static_assert(UW >= UA && UA >= 2 && kWait <= 63, "ring sizes");
   static_assert(MT >= 1 && MT <= 4 && kCap <= 64, "1 to 4 activation tiles");
+  static_assert(kPairs * 1024 <= kWave, "the end-of-kernel sum fits in the slots");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[WK * kWave];
 
   const int lane = threadIdx.x & 63;
@@ -537,7 +549,7 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
   const int M = a.m, N = a.n, K = a.k;
   const int KG = K >> 7;
   const int NB = (N + 127) >> 7;
-  const int n0 = blockIdx.x * 16;
+  const int n0 = blockIdx.x * (16 * NT);
   // activation rows [m0, mend); the expert's weights and scales when grouped
   int m0, mend;
   const uint8_t* bq = a.bq;
@@ -553,7 +565,11 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
     m0 = blockIdx.y * (16 * MT);
     mend = M;
   }
-  const int gw0 = wk * KG / WK, gw1 = (wk + 1) * KG / WK;
+  // split z (grid z) covers the scale groups [gz0, gz1); the waves split those
+  const int split = gridDim.z, z = blockIdx.z;
+  const int gz0 = (int)((int64_t)z * KG / split), gz1 = (int)((int64_t)(z + 1) * KG / split);
+  const int cz = gz1 - gz0;
+  const int gw0 = gz0 + wk * cz / WK, gw1 = gz0 + (wk + 1) * cz / WK;
   const int cnt = gw1 - gw0;
   const int rsub = lane & 15, c0 = lane >> 4;
   const int lrow = lane >> 3;
@@ -565,13 +581,15 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
   const float* const sa_l = reinterpret_cast<const float*>(wave_lds + UW * kW + UA * kA);
   const float* const sb_l = sa_l + kSaF;
 
-  f32x4 acc[MT];
+  f32x4 acc[NT][MT];
 #pragma unroll
-  for (int j = 0; j < MT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int j = 0; j < MT; ++j) acc[t][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   if (cnt > 0) {
     // rows past the end of A or B read as zeros
-    const u32x4 rB = rsrc_words(bq + (int64_t)n0 * K, (uint32_t)(min(16, N - n0) * K));
+    const u32x4 rB = rsrc_words(bq + (int64_t)n0 * K, (uint32_t)(min(16 * NT, N - n0) * K));
     const u32x4 rA = rsrc_words(a.aq + (int64_t)m0 * K, (uint32_t)(min(16 * MT, mend - m0) * K));
     const float* sb_src = bs + (int64_t)min(n0 >> 7, NB - 1) * KG + gw0;
     const float* sa_src = a.as + (int64_t)(m0 + min(lane % (16 * MT), mend - 1 - m0)) * KG + gw0;
@@ -589,19 +607,20 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
     auto issue_w = [&](int i) {  // group gw0 + i into weight slot i % UW
       const uint32_t dst = wbase + (uint32_t)(i % UW) * kW;
       if (i >= cnt) {
-        asm_global_to_lds4(sb_src, dst);
-        asm_global_to_lds4(sb_src, dst);
+#pragma unroll
+        for (int h = 0; h < 2 * NT; ++h) asm_global_to_lds4(sb_src, dst);
         return;
       }
       const int g = gw0 + i;
-      asm_buffer_to_lds16_nt(rB, dst, loff, g * 128);
-      asm_buffer_to_lds16_nt(rB, dst + 1024, loff, 8 * K + g * 128);
+#pragma unroll
+      for (int h = 0; h < 2 * NT; ++h)
+        asm_buffer_to_lds16_nt(rB, dst + h * 1024, loff, 8 * h * K + g * 128);
     };
     auto issue_a = [&](int i) {  // group gw0 + i into activation slot i % UA
       const uint32_t dst = abase + (uint32_t)(i % UA) * kA;
       if (i >= cnt) {
 #pragma unroll
-        for (int h = 0; h < kPerIter - 2; ++h) asm_global_to_lds4(sb_src, dst);
+        for (int h = 0; h < kPerIter - 2 * NT; ++h) asm_global_to_lds4(sb_src, dst);
         return;
       }
       const int g = gw0 + i;
@@ -629,16 +648,39 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
       asm volatile("" ::: "memory");
       const uint8_t* W = wave_lds + (i % UW) * kW;
       const uint8_t* A = wave_lds + UW * kW + (i % UA) * kA;
-      const i32x8 wop = lds_operand(W, rsub, c0);
       const float sb = PRE ? sb_l[i] : reinterpret_cast<const float*>(A + kOffSb)[0];
+      if constexpr (NT == 1) {
+        const i32x8 wop = lds_operand(W, rsub, c0);
 #pragma unroll
-      for (int j = 0; j < MT; ++j) {
-        const f32x4 pv = mfma_group(wop, lds_operand(A + j * 2048, rsub, c0));
-        const float sa = PRE ? sa_l[(16 * j + rsub) * cnt + i]
-                             : reinterpret_cast<const float*>(A + kOffSa)[16 * j + rsub];
-        const float sc = sa * sb;
+        for (int j = 0; j < MT; ++j) {
+          const f32x4 pv = mfma_group(wop, lds_operand(A + j * 2048, rsub, c0));
+          const float sa = PRE ? sa_l[(16 * j + rsub) * cnt + i]
+                               : reinterpret_cast<const float*>(A + kOffSa)[16 * j + rsub];
+          const float sc = sa * sb;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[j][r] = __builtin_fmaf(pv[r], sc, acc[j][r]);
+          for (int r = 0; r < 4; ++r) acc[0][j][r] = __builtin_fmaf(pv[r], sc, acc[0][j][r]);
+        }
+      } else {
+        // the MT activation slices once, then each weight slice against them
+        i32x8 aop[MT];
+        float sc[MT];
+#pragma unroll
+        for (int j = 0; j < MT; ++j) {
+          aop[j] = lds_operand(A + j * 2048, rsub, c0);
+          const float sa = PRE ? sa_l[(16 * j + rsub) * cnt + i]
+                               : reinterpret_cast<const float*>(A + kOffSa)[16 * j + rsub];
+          sc[j] = sa * sb;
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const i32x8 wop = lds_operand(W + t * 2048, rsub, c0);
+#pragma unroll
+          for (int j = 0; j < MT; ++j) {
+            const f32x4 pv = mfma_group(wop, aop[j]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[t][j][r] = __builtin_fmaf(pv[r], sc[j], acc[t][j][r]);
+          }
+        }
       }
       // the slots of group i are read (operands in registers) before refilling
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -648,23 +690,44 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
     __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm(0));  // tail loads have landed
   }
 
-  // sum the WK slices through LDS (the slots are free now); wave w adds up
-  // and stores tile w % MT
+  // Output block p = t * MT + j (weight slice t, activation tile j).  The WK
+  // slices are summed through LDS (the slots are free now) in wave order;
+  // wave w then owns blocks [w * kLP, (w + 1) * kLP).
+  f32x4 part[kLP];
   if constexpr (WK > 1) {
     __syncthreads();
-    f32x4* red = reinterpret_cast<f32x4*>(smem);  // [WK][MT][64]
+    f32x4* red = reinterpret_cast<f32x4*>(smem);  // [WK][kPairs][64]
 #pragma unroll
-    for (int j = 0; j < MT; ++j) red[(wk * MT + j) * 64 + lane] = acc[j];
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int j = 0; j < MT; ++j) red[(wk * kPairs + t * MT + j) * 64 + lane] = acc[t][j];
     __syncthreads();
-    for (int j = wk; j < MT; j += WK) {
-      f32x4 s = red[j * 64 + lane];
-      for (int w = 1; w < WK; ++w) s += red[(w * MT + j) * 64 + lane];
-      if (m0 + 16 * j + rsub < mend) store_out4<OUT_DT>(a, m0 + 16 * j + rsub, n0 + 4 * c0, s);
+#pragma unroll
+    for (int q = 0; q < kLP; ++q) {
+      const int p = wk * kLP + q;
+      if (p >= kPairs) continue;
+      f32x4 s = red[p * 64 + lane];
+      for (int w = 1; w < WK; ++w) s += red[(w * kPairs + p) * 64 + lane];
+      part[q] = s;
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < MT; ++j)
-      if (m0 + 16 * j + rsub < mend) store_out4<OUT_DT>(a, m0 + 16 * j + rsub, n0 + 4 * c0, acc[j]);
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int j = 0; j < MT; ++j) part[t * MT + j] = acc[t][j];
+  }
+  auto row_of = [&](int q) { return m0 + 16 * ((wk * kLP + q) % MT) + rsub; };
+  if (split > 1) {
+    const int tile = blockIdx.y * gridDim.x + blockIdx.x;
+    const int64_t tiles = (int64_t)gridDim.x * gridDim.y;
+    auto valid = [&](int q) { return wk * kLP + q < kPairs && row_of(q) < mend; };
+    if (!splitk_fixup<kLP>(a, part, split, z, tile, tiles, kPairs, wk * kLP, lane, valid)) return;
+  }
+#pragma unroll
+  for (int q = 0; q < kLP; ++q) {
+    const int p = wk * kLP + q;
+    if (p < kPairs && row_of(q) < mend)
+      store_out4<OUT_DT>(a, row_of(q), n0 + 16 * (p / MT) + 4 * c0, part[q]);
   }
 }
 
@@ -1497,6 +1560,18 @@ struct CfgEntry {
    {gemm_decode_wide_kernel<MT, WK, UW, UA, false, kFp32, true>,                               \
     gemm_decode_wide_kernel<MT, WK, UW, UA, false, kFp16, true>,                               \
     gemm_decode_wide_kernel<MT, WK, UW, UA, false, kBf16, true>}}
+#define DECODE_WIDE_NCFG(NT, MT, WK, UW, UA, NAME)                                             \
+  {4,                                                                                          \
+   16 * NT,                                                                                    \
+   16 * MT,                                                                                    \
+   WK,                                                                                         \
+   NAME,                                                                                       \
+   {gemm_decode_wide_kernel<MT, WK, UW, UA, true, kFp32, false, NT>,                           \
+    gemm_decode_wide_kernel<MT, WK, UW, UA, true, kFp16, false, NT>,                           \
+    gemm_decode_wide_kernel<MT, WK, UW, UA, true, kBf16, false, NT>},                          \
+   {gemm_decode_wide_kernel<MT, WK, UW, UA, false, kFp32, false, NT>,                          \
+    gemm_decode_wide_kernel<MT, WK, UW, UA, false, kFp16, false, NT>,                          \
+    gemm_decode_wide_kernel<MT, WK, UW, UA, false, kBf16, false, NT>}}
 #define PERSIST_CFG(BN, BM, WN, WM, NAME)                                                      \
   {3,                                                                                          \
    BN,                                                                                         \
@@ -1544,6 +1619,11 @@ const CfgEntry kCfgs[] = {
     DECODE_WIDE_GCFG(1, 8, 3, 3, "dw_m16_k8_w3a3"),
     DECODE_WIDE_GCFG(1, 4, 3, 3, "dw_m16_k4_w3a3"),
     DECODE_WIDE_CFG(1, 8, 2, 2, "dw_m16_k8_w2a2"),
+    DECODE_WIDE_NCFG(4, 4, 4, 2, 2, "dw_n64_m64_k4_w2a2"),
+    DECODE_WIDE_NCFG(2, 4, 4, 2, 2, "dw_n32_m64_k4_w2a2"),
+    DECODE_WIDE_NCFG(4, 2, 4, 2, 2, "dw_n64_m32_k4_w2a2"),
+    DECODE_WIDE_NCFG(2, 1, 8, 3, 3, "dw_n32_m16_k8_w3a3"),
+    DECODE_WIDE_NCFG(2, 2, 8, 2, 2, "dw_n32_m32_k8_w2a2"),
 };
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
@@ -1707,12 +1787,12 @@ PersistPlan persist_plan(const CfgEntry& cf, int64_t tiles, int64_t kg, int64_t 
 // Workspace a launch of configuration cf with `split` K partitions needs
 // (0 without a split), and whether it fits the fixed capacity.
 int64_t workspace_bytes(const CfgEntry& cf, int64_t split, int64_t m, int64_t n) {
-  if (split <= 1 || cf.kind == 3 || cf.kind == 4) return 0;
+  if (split <= 1 || cf.kind == 3) return 0;
   const int64_t tiles = ((n + cf.bn - 1) / cf.bn) * ((m + cf.bm - 1) / cf.bm);
   return split * tiles * cf.bn * cf.bm * 4;
 }
 bool workspace_fits(const CfgEntry& cf, int64_t split, int64_t m, int64_t n) {
-  if (split <= 1 || cf.kind == 3 || cf.kind == 4) return true;
+  if (split <= 1 || cf.kind == 3) return true;
   const int64_t tiles = ((n + cf.bn - 1) / cf.bn) * ((m + cf.bm - 1) / cf.bm);
   return tiles <= INFEROP_SPLITK_WS_COUNTERS &&
          workspace_bytes(cf, split, m, n) <= (int64_t)INFEROP_SPLITK_WS_BYTES;
@@ -1778,7 +1858,7 @@ extern "C" int64_t inferop_hip_gemm_workspace_bytes(int32_t cfg, int32_t split, 
     return persist_plan(cf, tiles, k / 128, split, cus).ws_bytes;
   }
   const int64_t tiles = ((n + cf.bn - 1) / cf.bn) * ((m + cf.bm - 1) / cf.bm);
-  if (s > 1 && cf.kind != 3 && cf.kind != 4 && tiles > INFEROP_SPLITK_WS_COUNTERS) return -1;
+  if (s > 1 && cf.kind != 3 && tiles > INFEROP_SPLITK_WS_COUNTERS) return -1;
   return workspace_bytes(cf, s, m, n);
 }
 
@@ -1820,15 +1900,25 @@ int gemm_block(void* c, const uint8_t* a_q, const float* a_scales, const uint8_t
     hipLaunchKernelGGL(cf.fn[di], dim3((unsigned)tn, (unsigned)split, (unsigned)tm),
                        dim3(64 * cf.waves), 0, st, args);
   } else if (cf.kind == 4) {
-    // one workgroup per 16-row weight stripe and 16*MT activation rows, the
-    // whole K range (split_k is ignored); stripe and tile rows are addressed
-    // with 32-bit offsets.  The scale preload holds wide_scale_cap(MT) groups
-    // per wave; a longer range per wave takes the kernel without it.
-    if ((int64_t)cf.bm * k > 0x7FFFFFFF) return hipErrorInvalidValue;
-    if (tn > 0x7FFFFFFF || tm > 65535) return hipErrorInvalidConfiguration;
-    const int64_t per_wave = (kg + cf.waves - 1) / cf.waves;
+    // one workgroup per bn-row weight stripe group and 16*MT activation rows
+    // over the whole K range, or over one of split_k K ranges (grid z, split-K
+    // fixup); stripe and tile rows are addressed with 32-bit offsets.  The
+    // scale preload holds wide_scale_cap(MT) groups per wave; a longer range
+    // per wave takes the kernel without it.
+    if ((int64_t)cf.bm * k > 0x7FFFFFFF || (int64_t)cf.bn * k > 0x7FFFFFFF)
+      return hipErrorInvalidValue;
+    int split = launch->split_k < 1 ? 1 : launch->split_k;
+    if (split > kg) split = kg;
+    if (tn > 0x7FFFFFFF || tm > 65535 || split > 65535) return hipErrorInvalidConfiguration;
+    if (!workspace_fits(cf, split, m, n)) return hipErrorInvalidValue;
+    if (split > 1) {
+      hipError_t e = splitk_buffers(noalloc, st, &args.ws, &args.counters);
+      if (e != hipSuccess) return e;
+    }
+    const int64_t per_wave = ((kg + split - 1) / split + cf.waves - 1) / cf.waves;
     const KernelFn fn = per_wave <= wide_scale_cap(cf.bm / 16) ? cf.fn[di] : cf.fn_alt[di];
-    hipLaunchKernelGGL(fn, dim3((unsigned)tn, (unsigned)tm), dim3(64 * cf.waves), 0, st, args);
+    hipLaunchKernelGGL(fn, dim3((unsigned)tn, (unsigned)tm, (unsigned)split), dim3(64 * cf.waves),
+                       0, st, args);
   } else if (cf.kind == 3) {
     // persistent: an even number of scale groups, one workgroup per CU (two
     // for 128x128 tiles, whose LDS allows it); split_k > 1 cuts the tiles of

@@ -59,8 +59,8 @@ typedef struct {
   int32_t kind;   /* 1 = decode (16-row weight stripes), 2 = LDS-staged output tiles,
                      3 = persistent LDS-staged tiles (K/128 even; split_k > 1 cuts
                          the tiles of the last, partial round along K),
-                     4 = wide decode: a weight stripe over all of K with bm activation
-                         rows (split_k ignored) */
+                     4 = wide decode: bn weight rows over all of K (or one of split_k
+                         K ranges) with bm activation rows */
   const char* name;
   int32_t grouped; /* kind 2: has a grouped-expert variant */
 } inferop_gemm_cfg_info;
@@ -112,9 +112,10 @@ int inferop_hip_gemm_w8a8_block_grouped(void* c, const uint8_t* a_q, const float
 /* ---- measurement kernels for the bench's ceilings ----
  * read_stream: one plain read of `bytes` (a multiple of 16) from src by
  * `blocks` workgroups of 256 lanes; sink: one device uint32 of scratch.
- * mfma_loop: `blocks` workgroups of 4 waves, each wave issuing iters x 8
- * E4M3 MFMAs of 16x16x128 from registers (65536 flops each), with promote the
- * four scale-promotion FMAs per MFMA the GEMM adds. */
+ * mfma_loop: `blocks` workgroups of 4 waves, each wave issuing iters x 32
+ * E4M3 MFMAs of 16x16x128 from registers (65536 flops each; one wave's share
+ * of a 256x256 tile per scale group), with promote the four scale-promotion
+ * FMAs per MFMA the GEMM adds. */
 int inferop_hip_diag_read_stream(const void* src, int64_t bytes, int32_t blocks, uint32_t* sink,
                                  void* stream);
 int inferop_hip_diag_mfma_loop(int32_t iters, int32_t blocks, int32_t promote, uint32_t* sink,

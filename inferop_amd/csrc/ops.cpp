@@ -92,6 +92,11 @@ enum GemmCfg : int32_t {
   kDwM16K8 = 26,
   kDwM16K4 = 27,
   kDwM16K8W2 = 28,
+  kDwN64M64 = 29,
+  kDwN32M64 = 30,
+  kDwN64M32 = 31,
+  kDwN32M16 = 32,
+  kDwN32M32 = 33,
 };
 
 struct GemmChoice {
@@ -114,6 +119,32 @@ GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
     return split < 1 ? int64_t(1) : split;
   };
   const int64_t stripes = (n + 15) / 16;  // 16-row weight stripes
+  // Multi-stripe wide decode tiles: a workgroup owns 32 or 64 weight rows and
+  // 32 or 64 activation rows, so a CU reads the activations once per 32-64
+  // weight rows; K is split so that about one workgroup runs per CU (at least
+  // 8 scale groups per split).  Two activation tiles of one row group share
+  // the weight rows through L2 only when their workgroups land on the same
+  // XCD (row groups a multiple of 8 along N), else one 64-row activation tile.
+  const int64_t tx64 = (n + 63) / 64, tx32 = (n + 31) / 32;
+  auto nt_split = [&](int64_t tiles) {
+    int64_t sp = cus / tiles;
+    if (sp > kg / 8) sp = kg / 8;
+    return int32_t(sp < 1 ? 1 : sp);
+  };
+  if (m > 32 && m <= 64 && !huge_k) {
+    // one round of workgroups at most (one per CU); M=64, K=7168: N=4096
+    // 14.0 -> 12.3 us (64x32 tiles, split 2), N=2112 12.3 -> 10.3 us (32x64,
+    // split 3); K=2048, N=7168: 8.8 -> 7.4 us
+    if (tx64 % 8 == 0 && tx64 * ((m + 31) / 32) <= cus)
+      return {kDwN64M32, nt_split(tx64 * ((m + 31) / 32))};
+    if (tx64 % 8 != 0 && tx32 <= cus) return {kDwN32M64, nt_split(tx32)};
+  }
+  if (m > 64 && m <= 128 && !huge_k && kg <= 16 && tx64 % 8 == 0) {
+    // short K: one workgroup per 64 weight rows and 32 (or 64) activation rows
+    // (M=128, N=4096, K=512: 4.9 -> 4.4 us; N=7168, K=2048: 11.6 -> 10.3 us)
+    if (tx64 * ((m + 31) / 32) <= cus) return {kDwN64M32, 1};
+    if (tx64 * ((m + 63) / 64) <= cus) return {kDwN64M64, 1};
+  }
   if (m > 16 && m <= 64 && !huge_k) {
     // HBM-bound.  The wide decode kernel gives a workgroup one weight stripe
     // over the whole K range with the activation tiles of all M rows (no
@@ -196,17 +227,42 @@ GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
     if (split < 1) split = 1;
     return {cfg, int32_t(split)};
   }
-  // MFMA-bound: a 256x256 tile runs alone on a CU and does four 128x128
-  // tiles' work in about 1.5x their time (two 128x128 tiles share a CU).
-  // Count whole rounds of workgroups for both and take the cheaper one.  The
-  // 256x256 tiles run on the persistent kernel when K has an even number of
-  // scale groups (it keeps the pipeline going across a CU's tiles and drains
-  // their stores in the background).
+  // MFMA-bound.  The 256x256 tiles run on the persistent kernel when K has
+  // an even number of scale groups (it keeps the pipeline going across a
+  // CU's tiles and drains their stores in the background); the tiles of its
+  // last, partial round are cut along K into up to 8 pieces that run at once
+  // (their partials added by a second kernel) when the round time saved,
+  // kg * (1 - 1/S) group-rounds, exceeds the cost of writing and re-reading
+  // tail * S partial tiles of 256 KB (at ~5 TB/s, ~0.026 group-rounds each)
+  // plus ~2.4 group-rounds of fixed cost (a group-round of 256x256 tiles
+  // takes ~2.05 us on 256 CUs).  Measured on MI355X: M=4096, N=4608,
+  // K=7168 (288 tiles) 177 -> 138 us with S=8 (128x128 tiles: 161 us);
+  // M=512, N=7168, K=18432 (56 tiles) 220 -> 89 us with S=4 (128x128: 115-132
+  // us); M=8192, N=7168, K=2048 (896 tiles) 139 us unsplit, 143 us with S=2.
   const int64_t t256 = ((n + 255) / 256) * ((m + 255) / 256);
   const int64_t t128 = ((n + 127) / 128) * ((m + 127) / 128);
+  auto tail_split = [&]() -> int32_t {
+    const int64_t tail = t256 >= cus ? t256 % cus : t256;
+    if (tail == 0) return 1;
+    int64_t sp = cus / tail;
+    if (sp > 8) sp = 8;
+    if (sp > kg / 2) sp = kg / 2;
+    if (sp < 2) return 1;
+    const double saved = (double)kg * (1.0 - 1.0 / (double)sp);
+    const double cost = (double)(tail * sp) * 0.0256 + 2.4;
+    return saved > cost ? int32_t(sp) : 1;
+  };
+  // at least one whole round of 256x256 tiles, or a long K: the persistent
+  // 256x256 tiles (M=512, N=7168, K=18432 and M=1024: 89 / 150 us against
+  // 115-132 / 189 us on 128x128 tiles)
+  if (kg % 2 == 0 && (t256 >= cus || kg >= 96)) return {kPerN256M256, tail_split()};
+  // Otherwise: a 256x256 tile runs alone on a CU and does four 128x128 tiles'
+  // work in about 1.5x their time (two 128x128 tiles share a CU); count whole
+  // rounds of workgroups for both and take the cheaper one.
   const int64_t r256 = (t256 + cus - 1) / cus;
   const int64_t r128 = (t128 + 2 * cus - 1) / (2 * cus);
-  if (2 * r256 * 3 < 2 * 2 * r128) return {kg % 2 == 0 ? kPerN256M256 : kPreN256M256S2, 1};
+  if (2 * r256 * 3 < 2 * 2 * r128)
+    return kg % 2 == 0 ? GemmChoice{kPerN256M256, tail_split()} : GemmChoice{kPreN256M256S2, 1};
   // too few 128x128 tiles to fill the CUs: split K across workgroups, each
   // split keeping at least 16 scale groups (below that the fp32 partial
   // round trip costs more than the idle CUs) and at most four splits.

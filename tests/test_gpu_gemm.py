@@ -266,7 +266,9 @@ def test_persistent_tail_split(name):
 @pytest.mark.gpu
 @pytest.mark.parametrize("name", ["dw_m64_k4_w2a2", "dw_m64_k2_w4a2", "dw_m32_k4_w2a2",
                                   "dw_m16_k2_w8a8", "dw_m16_k8_w3a3", "dw_m16_k4_w3a3",
-                                  "dw_m16_k8_w2a2"])
+                                  "dw_m16_k8_w2a2", "dw_n64_m64_k4_w2a2", "dw_n32_m64_k4_w2a2",
+                                  "dw_n64_m32_k4_w2a2", "dw_n32_m16_k8_w3a3",
+                                  "dw_n32_m32_k8_w2a2"])
 def test_wide_decode_kernels(name):
     # one workgroup per 16-row weight stripe over all of K: ragged stripes,
     # several activation tiles (M past one tile), waves left without groups

@@ -187,10 +187,15 @@ def test_gemm_selection_covers_configs():
     assert sel(16, 7168, 18432) == ("dw_m16_k2_w8a8", 1)
     assert sel(32, 7168, 2048) == ("dw_m32_k4_w2a2", 1)
     assert sel(32, 4096, 7168) == ("dw_m32_k4_w2a2", 1)
-    assert sel(64, 7168, 2048) == ("dw_m64_k2_w4a2", 1)
-    assert sel(64, 4096, 7168) == ("dw_m64_k4_w2a2", 1)
-    assert sel(64, 2112, 7168) == ("pre_n128_m32_w8_s4", 7)
+    # 33 <= M <= 64: a workgroup per 64 (or 32) weight rows, K split to fill
+    # one round of CUs; two 32-row activation tiles only when N's 64-row
+    # groups are a multiple of 8 (the tiles of a row group share an XCD)
+    assert sel(64, 7168, 2048) == ("dw_n64_m32_k4_w2a2", 1)
+    assert sel(64, 4096, 7168) == ("dw_n64_m32_k4_w2a2", 2)
+    assert sel(64, 2112, 7168) == ("dw_n32_m64_k4_w2a2", 3)
     assert sel(64, 36864, 7168) == ("pre_n128_m64_w8_s4", 2)
+    assert sel(128, 7168, 2048) == ("dw_n64_m64_k4_w2a2", 1)
+    assert sel(128, 4096, 512) == ("dw_n64_m32_k4_w2a2", 1)
     # 256x256 prefill tiles run on the persistent kernel when K / 128 is even,
     # on the one-tile-per-workgroup kernel otherwise
     assert names[inferop_amd.gemm_select(4096, 7168, 16384)[0]] == "per_n256_m256_w8"
