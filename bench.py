@@ -687,14 +687,23 @@ def host_cpu():
     import shutil
     import subprocess
     model = ""
+    extra = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.lower().startswith(("model name", "cpu model", "processor model")):
+            key = line.split(":", 1)[0].strip().lower()
+            if key in ("model name", "cpu model", "processor model") and not model:
                 model = line.split(":", 1)[1].strip()
-                if model:
-                    break
+            elif key in ("vendor_id", "cpu family", "model", "stepping", "cache size") \
+                    and key not in extra:
+                extra[key] = line.split(":", 1)[1].strip()
+            elif not line.strip() and model:
+                break
     except OSError:
         pass
+    if extra:
+        # the model string alone can be generic under virtualisation
+        model = (model or "unknown model") + " (" + ", ".join(
+            f"{k} {v}" for k, v in extra.items()) + ")"
     if not model and shutil.which("lscpu"):
         try:
             out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
