@@ -190,26 +190,36 @@ __device__ __forceinline__ void store_out4(const GemmArgs& a, int m, int n, cons
 // pair_base .. pair_base+LP-1 of the tile's `pairs` pairs; valid(q) says
 // whether this lane's q-th pair carries data (inside M, owned by this wave).
 // Returns true in the workgroup that arrives last for the tile; `part` then
-// holds the sum over all splits, added in split order.  Element r of a lane's
-// pair q sits at float (q * 4 + r) * 64 + lane of the wave's slot, so every
-// store and load instruction covers 256 contiguous bytes (these accesses
-// bypass the non-coherent caches; scattered 4-byte ones cost whole lines).
+// holds the sum over all splits, added in split order.  A lane's pair q sits
+// at bytes (q * 64 + lane) * 16 of the wave's slot, so every store and load
+// instruction moves 1 KB of contiguous memory.
+//
+// The partials are written and read with the sc1 cache policy (agent scope:
+// past the CU's L1 and the XCD's non-coherent L2), as plain buffer accesses
+// rather than atomic ones: the compiler serializes atomic loads (a full
+// vmcnt(0) wait after each), which made the last workgroup's reads one round
+// trip per split and per register -- M=1, N=2112, K=7168 with split 2 cost
+// 12.5 us against 6.8 us unsplit.  Plain loads of all splits are issued
+// together and waited for once.
+constexpr int kSc1 = 16;  // buffer cache policy bit: sc1
+
 template <int LP, typename Valid>
 __device__ __forceinline__ bool splitk_fixup(const GemmArgs& a, f32x4 (&part)[LP], int split,
                                              int z, int tile, int64_t tiles, int pairs,
                                              int pair_base, int lane, Valid valid) {
   __shared__ int s_last;
-  const int64_t tile_floats = (int64_t)pairs * 256;
-  float* mine = a.ws + ((int64_t)z * tiles + tile) * tile_floats + (int64_t)pair_base * 256;
+  const __amdgpu_buffer_rsrc_t ws = make_rsrc(a.ws, (uint32_t)INFEROP_SPLITK_WS_BYTES);
+  // byte offsets: the host keeps split * tiles * pairs * 1 KB within the workspace
+  const int tile_bytes = pairs * 1024;
+  const int split_bytes = (int)(tiles * tile_bytes);
+  const int mine = z * split_bytes + tile * tile_bytes + pair_base * 1024 + lane * 16;
 #pragma unroll
   for (int q = 0; q < LP; ++q) {
     if (!valid(q)) continue;
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      __hip_atomic_store(mine + (q * 4 + r) * 64 + lane, part[q][r], __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, part[q]), ws, mine + q * 1024,
+                                           0, kSc1);
   }
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's device-coherent stores are acknowledged
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores are acknowledged
   __syncthreads();
   if (threadIdx.x == 0) {
     const int old = __hip_atomic_fetch_add(a.counters + tile, 1, __ATOMIC_RELAXED,
@@ -218,8 +228,11 @@ __device__ __forceinline__ bool splitk_fixup(const GemmArgs& a, f32x4 (&part)[LP
   }
   __syncthreads();
   if (!s_last) return false;
-  const float* base = a.ws + (int64_t)tile * tile_floats + (int64_t)pair_base * 256 + lane;
-  const int64_t split_floats = tiles * tile_floats;
+  const int base = tile * tile_bytes + pair_base * 1024 + lane * 16;
+  auto load = [&](int zz, int q) {
+    return __builtin_bit_cast(
+        f32x4, __builtin_amdgcn_raw_buffer_load_b128(ws, base + zz * split_bytes + q * 1024, 0, kSc1));
+  };
   if constexpr (LP > 8) {
     // large tiles (never split by the automatic choice): one pair at a time,
     // which keeps the kernel's register budget
@@ -227,23 +240,14 @@ __device__ __forceinline__ bool splitk_fixup(const GemmArgs& a, f32x4 (&part)[LP
     for (int q = 0; q < LP; ++q) {
       if (!valid(q)) continue;
       f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
-      for (int zz = 0; zz < split; ++zz) {
-        const float* src = base + zz * split_floats + q * 256;
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          sum[r] += __hip_atomic_load(src + r * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
+      for (int zz = 0; zz < split; ++zz) sum += load(zz, q);
       part[q] = sum;
     }
   } else {
     // The partials of ZB splits for QB pairs are loaded together before any
     // is added, so the loads travel in parallel rather than one split at a
     // time; each element still adds the splits in order 0, 1, ..., split - 1.
-    // No load is issued past the last split: reloading the last split's
-    // partial in the spare batch slots (device-coherent loads of one address,
-    // many times over) cost more than the whole fixup -- M=1, N=2112, K=7168
-    // on 16-row stripes with split 2: 16.9 us with the reloads, 9.6 us
-    // without.
+    // No load is issued past the last split.
     constexpr int QB = LP < 4 ? LP : 4;
     constexpr int ZB = (LP <= 2 ? 16 : 8) / QB;
     static_assert(LP % QB == 0, "pairs in whole batches");
@@ -257,24 +261,16 @@ __device__ __forceinline__ bool splitk_fixup(const GemmArgs& a, f32x4 (&part)[LP
 #pragma unroll
         for (int zb = 0; zb < ZB; ++zb) {
           if (z0 + zb >= split) break;  // split is uniform: no divergence
-          const int zz = z0 + zb;
 #pragma unroll
-          for (int qb = 0; qb < QB; ++qb) {
-            if (!valid(q0 + qb)) continue;
-            const float* src = base + zz * split_floats + (q0 + qb) * 256;
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              v[zb][qb][r] = __hip_atomic_load(src + r * 64, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-          }
+          for (int qb = 0; qb < QB; ++qb)
+            if (valid(q0 + qb)) v[zb][qb] = load(z0 + zb, q0 + qb);
         }
 #pragma unroll
         for (int zb = 0; zb < ZB; ++zb) {
           if (z0 + zb >= split) break;
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) sum[qb][r] += v[zb][qb][r];
+            if (valid(q0 + qb)) sum[qb] += v[zb][qb];
         }
       }
 #pragma unroll
@@ -529,19 +525,26 @@ __host__ __device__ constexpr int wide_scale_cap(int) { return 16; }
 // rows instead of once per 16.  With fewer stripes than CUs left, the K range
 // is split across workgroups (grid z) and the partials meet in the split-K
 // fixup.
-template <int MT, int WK, int UW, int UA, bool PRE, int OUT_DT, bool GROUPED = false, int NT = 1>
+//
+// AR = 8 (one activation tile, M <= 8 rows per workgroup): a tile is 8 rows,
+// one load per group instead of two; the MFMA's other 8 columns read stale
+// LDS and their outputs are never stored or summed into stored outputs (each
+// output column of the MFMA depends only on its own activation row).
+template <int MT, int WK, int UW, int UA, bool PRE, int OUT_DT, bool GROUPED = false, int NT = 1,
+          int AR = 16>
 __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
   static_assert(NT == 1 || NT == 2 || NT == 4 || NT == 8, "stripes inside one weight block");
   static_assert(NT == 1 || !GROUPED, "grouped mode streams one stripe");
+  static_assert(AR == 16 || (AR == 8 && MT == 1 && !GROUPED), "8-row tiles: one plain tile");
   constexpr int kW = NT * 2048;                       // 16 * NT weight rows x 128 B
   constexpr int kCap = wide_scale_cap(MT);
-  constexpr int kOffSa = MT * 2048;                   // in an activation slot (no PRE)
+  constexpr int kOffSa = MT * AR * 128;               // in an activation slot (no PRE)
   constexpr int kOffSb = kOffSa + 256;
-  constexpr int kA = MT * 2048 + (PRE ? 0 : 512);     // MT tiles (+ 64 sa + 64 sb)
+  constexpr int kA = MT * AR * 128 + (PRE ? 0 : 512); // MT tiles (+ 64 sa + 64 sb)
   constexpr int kSaF = PRE ? 16 * MT * kCap : 0;      // preloaded sa floats, [row][group]
   constexpr int kScale = PRE ? kSaF * 4 + 256 : 0;    // + up to 64 sb floats
   constexpr int kWave = UW * kW + UA * kA + kScale;
-  constexpr int kPerIter = 2 * NT + 2 * MT + (PRE ? 0 : 2);  // loads issued per group
+  constexpr int kPerIter = 2 * NT + (AR / 8) * MT + (PRE ? 0 : 2);  // loads issued per group
   constexpr int kPairs = NT * MT;                     // 16x16 output blocks
   constexpr int kLP = (kPairs + WK - 1) / WK;         // blocks per wave at the end
   constexpr int kWait = (UA - 1) * kPerIter;          // loads that may stay in flight
@@ -568,7 +571,7 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
     bq += (int64_t)e * N * K;
     bs += (int64_t)e * NB * KG;
   } else {
-    m0 = blockIdx.y * (16 * MT);
+    m0 = blockIdx.y * (AR * MT);
     mend = M;
   }
   // split z (grid z) covers the scale groups [gz0, gz1); the waves split those
@@ -578,6 +581,7 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
   const int gw0 = gz0 + wk * cz / WK, gw1 = gz0 + (wk + 1) * cz / WK;
   const int cnt = gw1 - gw0;
   const int rsub = lane & 15, c0 = lane >> 4;
+  const int arow = rsub % AR;  // activation slice row a lane reads (8-row tiles: again 0-7)
   const int lrow = lane >> 3;
   const int loff = lrow * K + ((lane & 7) ^ lrow) * 16;
   uint8_t* const wave_lds = smem + wk * kWave;
@@ -596,7 +600,7 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
   if (cnt > 0) {
     // rows past the end of A or B read as zeros
     const u32x4 rB = rsrc_words(bq + (int64_t)n0 * K, (uint32_t)(min(16 * NT, N - n0) * K));
-    const u32x4 rA = rsrc_words(a.aq + (int64_t)m0 * K, (uint32_t)(min(16 * MT, mend - m0) * K));
+    const u32x4 rA = rsrc_words(a.aq + (int64_t)m0 * K, (uint32_t)(min(AR * MT, mend - m0) * K));
     const float* sb_src = bs + (int64_t)min(n0 >> 7, NB - 1) * KG + gw0;
     const float* sa_src = a.as + (int64_t)(m0 + min(lane % (16 * MT), mend - 1 - m0)) * KG + gw0;
     if constexpr (PRE) {
@@ -631,7 +635,7 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
       }
       const int g = gw0 + i;
 #pragma unroll
-      for (int h = 0; h < 2 * MT; ++h)
+      for (int h = 0; h < (AR / 8) * MT; ++h)
         asm_buffer_to_lds16(rA, dst + h * 1024, loff, 8 * h * K + g * 128);
       if constexpr (!PRE) {
         asm_global_to_lds4(sa_src + i, dst + kOffSa);
@@ -659,7 +663,7 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
         const i32x8 wop = lds_operand(W, rsub, c0);
 #pragma unroll
         for (int j = 0; j < MT; ++j) {
-          const f32x4 pv = mfma_group(wop, lds_operand(A + j * 2048, rsub, c0));
+          const f32x4 pv = mfma_group(wop, lds_operand(A + j * AR * 128, arow, c0));
           const float sa = PRE ? sa_l[(16 * j + rsub) * cnt + i]
                                : reinterpret_cast<const float*>(A + kOffSa)[16 * j + rsub];
           const float sc = sa * sb;
@@ -672,7 +676,7 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
         float sc[MT];
 #pragma unroll
         for (int j = 0; j < MT; ++j) {
-          aop[j] = lds_operand(A + j * 2048, rsub, c0);
+          aop[j] = lds_operand(A + j * AR * 128, arow, c0);
           const float sa = PRE ? sa_l[(16 * j + rsub) * cnt + i]
                                : reinterpret_cast<const float*>(A + kOffSa)[16 * j + rsub];
           sc[j] = sa * sb;
@@ -723,16 +727,17 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
       for (int j = 0; j < MT; ++j) part[t * MT + j] = acc[t][j];
   }
   auto row_of = [&](int q) { return m0 + 16 * ((wk * kLP + q) % MT) + rsub; };
+  const bool lane_row = AR == 16 || rsub < AR;  // with 8-row tiles, lanes of rows 8-15 hold no row
   if (split > 1) {
     const int tile = blockIdx.y * gridDim.x + blockIdx.x;
     const int64_t tiles = (int64_t)gridDim.x * gridDim.y;
-    auto valid = [&](int q) { return wk * kLP + q < kPairs && row_of(q) < mend; };
+    auto valid = [&](int q) { return wk * kLP + q < kPairs && lane_row && row_of(q) < mend; };
     if (!splitk_fixup<kLP>(a, part, split, z, tile, tiles, kPairs, wk * kLP, lane, valid)) return;
   }
 #pragma unroll
   for (int q = 0; q < kLP; ++q) {
     const int p = wk * kLP + q;
-    if (p < kPairs && row_of(q) < mend)
+    if (p < kPairs && lane_row && row_of(q) < mend)
       store_out4<OUT_DT>(a, row_of(q), n0 + 16 * (p / MT) + 4 * c0, part[q]);
   }
 }
@@ -1569,6 +1574,18 @@ struct CfgEntry {
    {gemm_decode_wide_kernel<MT, WK, UW, UA, false, kFp32, true>,                               \
     gemm_decode_wide_kernel<MT, WK, UW, UA, false, kFp16, true>,                               \
     gemm_decode_wide_kernel<MT, WK, UW, UA, false, kBf16, true>}}
+#define DECODE_WIDE_M8CFG(WK, UW, UA, NAME)                                                    \
+  {4,                                                                                          \
+   16,                                                                                         \
+   8,                                                                                          \
+   WK,                                                                                         \
+   NAME,                                                                                       \
+   {gemm_decode_wide_kernel<1, WK, UW, UA, true, kFp32, false, 1, 8>,                          \
+    gemm_decode_wide_kernel<1, WK, UW, UA, true, kFp16, false, 1, 8>,                          \
+    gemm_decode_wide_kernel<1, WK, UW, UA, true, kBf16, false, 1, 8>},                         \
+   {gemm_decode_wide_kernel<1, WK, UW, UA, false, kFp32, false, 1, 8>,                         \
+    gemm_decode_wide_kernel<1, WK, UW, UA, false, kFp16, false, 1, 8>,                         \
+    gemm_decode_wide_kernel<1, WK, UW, UA, false, kBf16, false, 1, 8>}}
 #define DECODE_WIDE_NCFG(NT, MT, WK, UW, UA, NAME)                                             \
   {4,                                                                                          \
    16 * NT,                                                                                    \
@@ -1633,6 +1650,8 @@ const CfgEntry kCfgs[] = {
     DECODE_WIDE_NCFG(4, 2, 4, 2, 2, "dw_n64_m32_k4_w2a2"),
     DECODE_WIDE_NCFG(2, 1, 8, 3, 3, "dw_n32_m16_k8_w3a3"),
     DECODE_WIDE_NCFG(2, 2, 8, 2, 2, "dw_n32_m32_k8_w2a2"),
+    DECODE_WIDE_M8CFG(8, 4, 4, "dw_m8_k8_w4a4"),
+    DECODE_WIDE_M8CFG(4, 4, 4, "dw_m8_k4_w4a4"),
 };
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 

@@ -31,7 +31,7 @@ void check(bool ok, const char* what) {
   }
 }
 int32_t g_last_cfg = -1, g_last_split = -1;
-constexpr int kStubConfigs = 34;
+constexpr int kStubConfigs = 36;
 }  // namespace
 
 // ---- stand-ins for the HIP launch layer (hip_launch.h) ----------------------

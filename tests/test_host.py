@@ -179,10 +179,15 @@ def test_gemm_selection_covers_configs():
     def sel(m, n, k):
         cfg, split = inferop_amd.gemm_select(m, n, k)
         return names[cfg], split
-    assert sel(1, 7168, 2048) == ("dw_m16_k4_w3a3", 1)
-    assert sel(1, 4096, 7168) == ("dw_m16_k8_w3a3", 1)
+    # M <= 8: 8-row activation tiles
+    assert sel(1, 7168, 2048) == ("dw_m8_k4_w4a4", 1)
+    assert sel(1, 4096, 7168) == ("dw_m8_k8_w4a4", 1)
+    assert sel(8, 2112, 7168) == ("dw_m8_k8_w4a4", 1)
+    assert sel(1, 7168, 7168) == ("dw_m8_k4_w4a4", 1)
+    assert sel(16, 7168, 2048) == ("dw_m16_k4_w3a3", 1)
+    assert sel(16, 4096, 7168) == ("dw_m16_k8_w3a3", 1)
     assert sel(16, 2112, 7168) == ("dw_m16_k8_w3a3", 1)
-    assert sel(1, 7168, 7168) == ("dw_m16_k4_w3a3", 1)
+    assert sel(16, 7168, 7168) == ("dw_m16_k4_w3a3", 1)
     assert sel(16, 36864, 7168) == ("dw_m16_k8_w2a2", 1)
     assert sel(16, 7168, 18432) == ("dw_m16_k2_w8a8", 1)
     assert sel(32, 7168, 2048) == ("dw_m32_k4_w2a2", 1)
