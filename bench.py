@@ -303,6 +303,29 @@ def main():
         launch_floor_us = time_graphs([gl], 10) / PER_KERNEL_LAUNCHES * 1e3
         del gl
 
+        # The decode kernels' unit of work measured without the GEMM: one
+        # 8-wave workgroup per 16-row weight stripe, every load of a workgroup
+        # in flight at once, in four access patterns, from HBM (the rotating
+        # weight copies) and L2-resident (workgroup i reads stripe i % 16):
+        # what the load path itself allows per compute unit.
+        patterns = ("rows8_regs", "contig_regs", "mfma_layout_regs", "rows8_lds_dma")
+        stripe_reads = []
+        for (n, k) in DECODE_NK:
+            for src, stripes in (("hbm", 0), ("l2", 16)):
+                for pat, pname in enumerate(patterns):
+                    gr = capture(lambda: [ia.diag_stripe_read(W[(n, k)][r % R][0], n, k, pat,
+                                                              stripes, sink, sp)
+                                          for r in range(PER_KERNEL_LAUNCHES)])
+                    time_graphs([gr], 4)
+                    t = time_graphs([gr], 10) / PER_KERNEL_LAUNCHES
+                    del gr
+                    stripe_reads.append({
+                        "n": n, "k": k, "source": src, "pattern": pname,
+                        "us": round(t * 1e3, 2),
+                        "tbs": round(n * k / (t * 1e-3) / 1e12, 2),
+                        "per_workgroup_gbs_above_floor": round(
+                            16 * k / max(t * 1e3 - launch_floor_us, 1e-3) / 1e3, 1)})
+
         # per-kernel: a graph of PER_KERNEL_LAUNCHES back-to-back launches
         detail = []
         g_bytes = g_ms = q_bytes = q_ms = 0.0
@@ -355,6 +378,11 @@ def main():
                         "same rotating weight copies, timed like the GEMM (graph of 20 "
                         "launches); gemm_frac_of_stream_ceiling = stream_read_us / gemm_us",
                 "launch_floor_us": round(launch_floor_us, 2),
+                "stripe_reads": stripe_reads,
+                "stripe_reads_what": "inferop_diag_stripe_read: one 8-wave workgroup per 16-row "
+                                     "stripe (workgroup bytes 16*K), all loads in flight; "
+                                     "per_workgroup_gbs_above_floor = 16*K / (us - "
+                                     "launch_floor_us)",
                 "gemm_frac_of_stream_ceiling_mean": round(
                     sum(d["gemm_frac_of_stream_ceiling"] for d in detail) / len(detail), 4)},
             "quant_decode_gbs": round(q_bytes / (q_ms * 1e-3) / 1e9, 1),

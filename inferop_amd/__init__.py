@@ -8,7 +8,7 @@ Python (``inferop_amd.ops``, same names as the reference's operators).
 from ._lib import LIB_PATH, LibraryNotBuilt, lib  # noqa: F401
 from .ops import (  # noqa: F401
     dequant_fp8_per_token_group, dequantize, device_count, device_name, device_sm_version,
-    diag_mfma_loop, diag_read_stream, dtype, fused_add_rmsnorm_quant_fp8, gemm,
+    diag_mfma_loop, diag_read_stream, diag_stripe_read, dtype, fused_add_rmsnorm_quant_fp8, gemm,
     gemm_config_name, gemm_num_configs, gemm_select, grouped_gemm_masked_select,
     grouped_gemm_select, has_cuda, InferopError, quant_fp8_per_token_group,
     quant_fp8_weight_block, quantize, quantize_weight, silu_and_mul_quant_fp8, Status,

@@ -57,6 +57,7 @@ C_API = [
     ("inferop_selftest_fp8_codec", ctypes.c_int, [_u64, _u64, _vp, _vp]),
     ("inferop_diag_read_stream", ctypes.c_int, [_vp, _i64, _i32, _vp, _vp]),
     ("inferop_diag_mfma_loop", ctypes.c_int, [_i32, _i32, _i32, _vp, _vp]),
+    ("inferop_diag_stripe_read", ctypes.c_int, [_vp, _i64, _i64, _i32, _i32, _vp, _vp]),
 ]
 
 _lib = None

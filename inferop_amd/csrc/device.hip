@@ -195,7 +195,108 @@ __global__ __launch_bounds__(256) void mfma_loop_kernel(int iters, uint32_t magi
   if (__builtin_bit_cast(uint32_t, t) == magic) sink[0] = magic;
 }
 
+// One read of a [n, k] byte matrix by one workgroup of 8 waves per 16-row
+// stripe, every load of the workgroup in flight at once (wave w takes scale
+// groups [w*G, w*G + G) of the stripe's 16 rows, G = k / 1024), in one of the
+// access patterns the decode GEMM kernels could use:
+//   0: register loads, each instruction 8 rows x 128 B (the decode kernels'
+//      row pattern: 8 lanes per 128-byte row segment)
+//   1: register loads, each instruction 1 KB contiguous
+//   2: register loads in the MFMA operand layout (lane l: row l % 16, 16 bytes
+//      at chunk l / 16 of the group, then chunk l / 16 + 4): 16 rows x 64 B
+//      per instruction
+//   3: direct global->LDS loads, 8 rows x 128 B per instruction (the decode
+//      kernels' loads), read back from LDS after one wait
+// With `stripes` > 0 workgroup b reads stripe b % stripes, so the data stays
+// in L2 after the first touch and the launch measures a CU's load throughput
+// rather than HBM.  The loaded words feed a XOR stored only when it equals
+// `magic` (never, in practice), so no load can be dropped.
+template <int P, int G>
+__global__ __launch_bounds__(512) void stripe_read_kernel(const uint8_t* __restrict__ b, int k,
+                                                          int stripes, uint32_t magic,
+                                                          uint32_t* sink) {
+  constexpr int L = 2 * G;  // 1 KB loads per wave
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[P == 3 ? 8 * L * 1024 : 16];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int sidx = stripes > 0 ? (int)(blockIdx.x % (unsigned)stripes) : (int)blockIdx.x;
+  const uint8_t* s = b + (int64_t)sidx * 16 * k;
+  u32x4 v[L];
+  if constexpr (P == 0 || P == 3) {
+    const int lrow = lane >> 3, ch = lane & 7;
+    if constexpr (P == 0) {
+#pragma unroll
+      for (int i = 0; i < G; ++i)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          v[2 * i + h] = __builtin_nontemporal_load(
+              reinterpret_cast<const u32x4*>(s + (8 * h + lrow) * k + (w * G + i) * 128 + ch * 16));
+    } else {
+      const __amdgpu_buffer_rsrc_t r =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(s), (short)0, 16 * k, 0x00020000);
+#pragma unroll
+      for (int i = 0; i < G; ++i)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              r, (__attribute__((address_space(3))) void*)(lds + (w * L + 2 * i + h) * 1024), 16,
+              (8 * h + lrow) * k + (w * G + i) * 128 + (ch ^ lrow) * 16, 0, 0, 2);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < L; ++i)
+        v[i] = *reinterpret_cast<const u32x4*>(lds + (w * L + i) * 1024 + lane * 16);
+    }
+  } else if constexpr (P == 1) {
+#pragma unroll
+    for (int i = 0; i < L; ++i)
+      v[i] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4*>(s + (int64_t)(i * 8 + w) * 1024 + lane * 16));
+  } else {
+    const int r = lane & 15, c0 = lane >> 4;
+#pragma unroll
+    for (int i = 0; i < G; ++i)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        v[2 * i + h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+            s + r * k + (w * G + i) * 128 + (c0 + 4 * h) * 16));
+  }
+  uint32_t x = 0;
+#pragma unroll
+  for (int i = 0; i < L; ++i) x ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+  if (x == magic) sink[0] = x;
+}
+
+template <int G>
+hipError_t launch_stripe_read(int pattern, const uint8_t* b, int64_t n, int64_t k, int stripes,
+                              uint32_t* sink, hipStream_t st) {
+  const dim3 grid((unsigned)(n / 16)), block(512);
+  const uint32_t magic = 0x9E3779B9u;
+  switch (pattern) {
+    case 0: hipLaunchKernelGGL((stripe_read_kernel<0, G>), grid, block, 0, st, b, (int)k, stripes, magic, sink); break;
+    case 1: hipLaunchKernelGGL((stripe_read_kernel<1, G>), grid, block, 0, st, b, (int)k, stripes, magic, sink); break;
+    case 2: hipLaunchKernelGGL((stripe_read_kernel<2, G>), grid, block, 0, st, b, (int)k, stripes, magic, sink); break;
+    default: hipLaunchKernelGGL((stripe_read_kernel<3, G>), grid, block, 0, st, b, (int)k, stripes, magic, sink); break;
+  }
+  return hipGetLastError();
+}
+
 }  // namespace
+
+extern "C" int inferop_hip_diag_stripe_read(const void* b, int64_t n, int64_t k, int32_t pattern,
+                                            int32_t stripes, uint32_t* sink, void* stream) {
+  // one workgroup per 16 rows, G = k / 1024 groups of 128 bytes per wave
+  if (!b || !sink || n < 16 || n % 16 != 0 || n / 16 > 65535 || k % 1024 != 0 || pattern < 0 ||
+      pattern > 3 || stripes < 0 || (stripes > 0 && stripes > n / 16) || 16 * k > 0x7FFFFFFF)
+    return hipErrorInvalidValue;
+  const auto u8 = static_cast<const uint8_t*>(b);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (k / 1024) {
+    case 2: return launch_stripe_read<2>(pattern, u8, n, k, stripes, sink, st);
+    case 7: return launch_stripe_read<7>(pattern, u8, n, k, stripes, sink, st);
+    case 8: return launch_stripe_read<8>(pattern, u8, n, k, stripes, sink, st);
+    default: return hipErrorInvalidValue;
+  }
+}
 
 extern "C" int inferop_hip_diag_read_stream(const void* src, int64_t bytes, int32_t blocks,
                                             uint32_t* sink, void* stream) {

@@ -1298,6 +1298,15 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_persist_kernel(GemmArgs a) 
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
     };
+    // the output passes only synchronize LDS: no wait for vector memory (the
+    // next unit's first group has landed at the barrier before them, and the
+    // stores of C need not complete)
+    auto lds_barrier = [&]() {
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm(63));
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    };
     const int l = kLoader ? wave : 0;
     u32x4 rB = u32x4{0u, 0u, 0u, 0u}, rA = u32x4{0u, 0u, 0u, 0u};
     const float* sa_src = a.as;
@@ -1417,7 +1426,7 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_persist_kernel(GemmArgs a) 
             }
           }
         }
-        barrier();  // the pass is in LDS
+        lds_barrier();  // the pass is in LDS
         if constexpr (!kLoader) {
           // four pieces at a time: the accumulators of later passes are live
           constexpr int QB = kPieces < 4 ? kPieces : 4;
@@ -1446,7 +1455,7 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_persist_kernel(GemmArgs a) 
             }
           }
         }
-        barrier();  // the storing waves have read the pass out of LDS
+        lds_barrier();  // the storing waves have read the pass out of LDS
       }
       if (!has_next) break;
       u = nu;

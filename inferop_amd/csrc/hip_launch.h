@@ -120,6 +120,13 @@ int inferop_hip_diag_read_stream(const void* src, int64_t bytes, int32_t blocks,
                                  void* stream);
 int inferop_hip_diag_mfma_loop(int32_t iters, int32_t blocks, int32_t promote, uint32_t* sink,
                                void* stream);
+/* stripe_read: one read of the [n, k] byte matrix b by one 8-wave workgroup
+ * per 16-row stripe, all of a workgroup's loads in flight, in access pattern
+ * 0-3 (8-row register loads, contiguous register loads, MFMA-layout register
+ * loads, 8-row direct-to-LDS loads); stripes > 0 makes workgroup i read
+ * stripe i % stripes (L2-resident).  n % 16 == 0, k / 1024 in {2, 7, 8}. */
+int inferop_hip_diag_stripe_read(const void* b, int64_t n, int64_t k, int32_t pattern,
+                                 int32_t stripes, uint32_t* sink, void* stream);
 
 /* ---- device self-test of the E4M3 conversions used by the fast paths ----
  * counts[0]: fp32 patterns in [lo, hi) inside the quantizer fast-path domain

@@ -805,6 +805,18 @@ extern "C" int inferop_diag_read_stream(const void* src, int64_t bytes, int32_t 
       inferop_hip_diag_read_stream(src, bytes, blocks, static_cast<uint32_t*>(sink), stream));
 }
 
+extern "C" int inferop_diag_stripe_read(const void* b, int64_t n, int64_t k, int32_t pattern,
+                                        int32_t stripes, void* sink, void* stream) {
+  if (!current_device()) return INFEROP_ERR_DEVICE;
+  const int64_t g = k / 1024;
+  if (!b || !sink || n < 16 || n % 16 != 0 || n / 16 > 65535 || k % 1024 != 0 ||
+      (g != 2 && g != 7 && g != 8) || pattern < 0 || pattern > 3 || stripes < 0 ||
+      stripes > n / 16)
+    return INFEROP_ERR_ARGUMENT;
+  return status_of_hip(inferop_hip_diag_stripe_read(b, n, k, pattern, stripes,
+                                                    static_cast<uint32_t*>(sink), stream));
+}
+
 extern "C" int inferop_diag_mfma_loop(int32_t iters, int32_t blocks, int32_t promote, void* sink,
                                       void* stream) {
   if (!gemm_device()) return INFEROP_ERR_DEVICE;

@@ -231,6 +231,14 @@ def diag_read_stream(src, nbytes: int, blocks: int, sink, stream=None) -> int:
     return lib().inferop_diag_read_stream(_ptr(src), nbytes, blocks, _ptr(sink), _stream(stream))
 
 
+def diag_stripe_read(b, n: int, k: int, pattern: int, stripes: int, sink, stream=None) -> int:
+    """One read of the [n, k] bytes of b, one 8-wave workgroup per 16-row
+    stripe, all loads in flight, in access pattern 0-3; stripes > 0 keeps the
+    data L2-resident (a compute unit's load rate)."""
+    return lib().inferop_diag_stripe_read(_ptr(b), n, k, pattern, stripes, _ptr(sink),
+                                          _stream(stream))
+
+
 def diag_mfma_loop(iters: int, blocks: int, promote: bool, sink, stream=None) -> int:
     """The GEMM's MFMA inner loop from registers (the matrix-core ceiling)."""
     return lib().inferop_diag_mfma_loop(iters, blocks, 1 if promote else 0, _ptr(sink),

@@ -129,6 +129,13 @@ int inferop_hip_diag_read_stream(const void*, int64_t bytes, int32_t blocks, uin
   check(bytes >= 16 && bytes % 16 == 0 && blocks >= 1, "read stream args");
   return 0;
 }
+int inferop_hip_diag_stripe_read(const void*, int64_t n, int64_t k, int32_t pattern,
+                                 int32_t stripes, uint32_t*, void*) {
+  check(n >= 16 && n % 16 == 0 && (k == 2048 || k == 7168 || k == 8192) && pattern >= 0 &&
+            pattern <= 3 && stripes >= 0 && stripes <= n / 16,
+        "stripe read args");
+  return 0;
+}
 int inferop_hip_diag_mfma_loop(int32_t iters, int32_t blocks, int32_t, uint32_t*, void*) {
   check(iters >= 1 && blocks >= 1, "mfma loop args");
   return 0;
@@ -214,6 +221,14 @@ void host_layer() {
             INFEROP_ERR_ARGUMENT,
         "forced split beyond the workspace");
   check(inferop_diag_read_stream(d, 8, 1, d, nullptr) == INFEROP_ERR_ARGUMENT, "read 8 bytes");
+  check(inferop_diag_stripe_read(d, 4096, 3072, 0, 0, d, nullptr) == INFEROP_ERR_ARGUMENT,
+        "stripe read k");
+  check(inferop_diag_stripe_read(d, 100, 2048, 0, 0, d, nullptr) == INFEROP_ERR_ARGUMENT,
+        "stripe read n");
+  check(inferop_diag_stripe_read(d, 4096, 7168, 4, 0, d, nullptr) == INFEROP_ERR_ARGUMENT,
+        "stripe read pattern");
+  check(inferop_diag_stripe_read(d, 4096, 7168, 3, 16, d, nullptr) == INFEROP_OK,
+        "stripe read resident");
   check(std::strcmp(inferop_status_string(99), "unknown status") == 0, "status text");
 }
 
