@@ -308,7 +308,8 @@ def main():
         # in flight at once, in four access patterns, from HBM (the rotating
         # weight copies) and L2-resident (workgroup i reads stripe i % 16):
         # what the load path itself allows per compute unit.
-        patterns = ("rows8_regs", "contig_regs", "mfma_layout_regs", "rows8_lds_dma")
+        patterns = ("rows8_regs", "contig_regs", "mfma_layout_regs", "rows8_lds_dma",
+                    "rows8_regs_to_lds")
         stripe_reads = []
         for (n, k) in DECODE_NK:
             for src, stripes in (("hbm", 0), ("l2", 16)):

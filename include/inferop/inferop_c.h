@@ -199,7 +199,8 @@ int inferop_diag_mfma_loop(int32_t iters, int32_t blocks, int32_t promote, void*
  * 0 register loads of 8 rows x 128 B per instruction, 1 register loads of
  * 1 KB contiguous, 2 register loads in the MFMA operand layout (16 rows x 64 B
  * per instruction), 3 direct global->LDS loads of 8 rows x 128 B (the decode
- * kernels' loads).  stripes > 0: workgroup i reads stripe i % stripes, so the
+ * kernels' loads), 4 pattern 0's register loads written to LDS with
+ * ds_write_b128 in pattern 3's layout.  stripes > 0: workgroup i reads stripe i % stripes, so the
  * data is L2-resident and the launch measures a compute unit's load rate.
  * n a multiple of 16, k / 1024 in {2, 7, 8}; sink: one device uint32. */
 int inferop_diag_stripe_read(const void* b, int64_t n, int64_t k, int32_t pattern,

@@ -207,6 +207,8 @@ __global__ __launch_bounds__(256) void mfma_loop_kernel(int iters, uint32_t magi
 //      per instruction
 //   3: direct global->LDS loads, 8 rows x 128 B per instruction (the decode
 //      kernels' loads), read back from LDS after one wait
+//   4: pattern 0's register loads written to LDS (ds_write_b128, the layout
+//      pattern 3 leaves) and read back, i.e. the register path into LDS
 // With `stripes` > 0 workgroup b reads stripe b % stripes, so the data stays
 // in L2 after the first touch and the launch measures a CU's load throughput
 // rather than HBM.  The loaded words feed a XOR stored only when it equals
@@ -216,14 +218,28 @@ __global__ __launch_bounds__(512) void stripe_read_kernel(const uint8_t* __restr
                                                           int stripes, uint32_t magic,
                                                           uint32_t* sink) {
   constexpr int L = 2 * G;  // 1 KB loads per wave
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[P == 3 ? 8 * L * 1024 : 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[P >= 3 ? 8 * L * 1024 : 16];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int sidx = stripes > 0 ? (int)(blockIdx.x % (unsigned)stripes) : (int)blockIdx.x;
   const uint8_t* s = b + (int64_t)sidx * 16 * k;
   u32x4 v[L];
-  if constexpr (P == 0 || P == 3) {
+  if constexpr (P == 0 || P == 3 || P == 4) {
     const int lrow = lane >> 3, ch = lane & 7;
-    if constexpr (P == 0) {
+    if constexpr (P == 4) {
+#pragma unroll
+      for (int i = 0; i < G; ++i)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          v[2 * i + h] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+              s + (8 * h + lrow) * k + (w * G + i) * 128 + (ch ^ lrow) * 16));
+#pragma unroll
+      for (int i = 0; i < L; ++i)
+        *reinterpret_cast<u32x4*>(lds + (w * L + i) * 1024 + lane * 16) = v[i];
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < L; ++i)
+        v[i] = *reinterpret_cast<const u32x4*>(lds + (w * L + (i + 1) % L) * 1024 + lane * 16);
+    } else if constexpr (P == 0) {
 #pragma unroll
       for (int i = 0; i < G; ++i)
 #pragma unroll
@@ -275,7 +291,8 @@ hipError_t launch_stripe_read(int pattern, const uint8_t* b, int64_t n, int64_t 
     case 0: hipLaunchKernelGGL((stripe_read_kernel<0, G>), grid, block, 0, st, b, (int)k, stripes, magic, sink); break;
     case 1: hipLaunchKernelGGL((stripe_read_kernel<1, G>), grid, block, 0, st, b, (int)k, stripes, magic, sink); break;
     case 2: hipLaunchKernelGGL((stripe_read_kernel<2, G>), grid, block, 0, st, b, (int)k, stripes, magic, sink); break;
-    default: hipLaunchKernelGGL((stripe_read_kernel<3, G>), grid, block, 0, st, b, (int)k, stripes, magic, sink); break;
+    case 3: hipLaunchKernelGGL((stripe_read_kernel<3, G>), grid, block, 0, st, b, (int)k, stripes, magic, sink); break;
+    default: hipLaunchKernelGGL((stripe_read_kernel<4, G>), grid, block, 0, st, b, (int)k, stripes, magic, sink); break;
   }
   return hipGetLastError();
 }
@@ -286,7 +303,7 @@ extern "C" int inferop_hip_diag_stripe_read(const void* b, int64_t n, int64_t k,
                                             int32_t stripes, uint32_t* sink, void* stream) {
   // one workgroup per 16 rows, G = k / 1024 groups of 128 bytes per wave
   if (!b || !sink || n < 16 || n % 16 != 0 || n / 16 > 65535 || k % 1024 != 0 || pattern < 0 ||
-      pattern > 3 || stripes < 0 || (stripes > 0 && stripes > n / 16) || 16 * k > 0x7FFFFFFF)
+      pattern > 4 || stripes < 0 || (stripes > 0 && stripes > n / 16) || 16 * k > 0x7FFFFFFF)
     return hipErrorInvalidValue;
   const auto u8 = static_cast<const uint8_t*>(b);
   hipStream_t st = static_cast<hipStream_t>(stream);

@@ -509,11 +509,11 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_lds_kernel(GemmArgs a) {
 // weight scales for all its groups into LDS once, before the rings start, as
 // row-contiguous runs (a per-group load of 16*MT activation scales touches
 // 16*MT cache lines, more than the weight slice itself).  That needs at most
-// wide_scale_cap(MT) groups per wave; longer ranges use the kernel without
+// wide_scale_cap() groups per wave; longer ranges use the kernel without
 // PRE, whose activation slots also carry that group's scales.  The cap keeps
 // the configurations small enough for two workgroups per CU (LDS), which is
 // worth more than preloading for longer K.
-__host__ __device__ constexpr int wide_scale_cap(int) { return 16; }
+__host__ __device__ constexpr int wide_scale_cap() { return 16; }
 
 // Grouped mode (GROUPED): grid y enumerates virtual M tiles of 16*MT rows as in
 // the tiled kernel's grouped mode (grouped_tile); a workgroup streams one
@@ -537,7 +537,7 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
   static_assert(NT == 1 || !GROUPED, "grouped mode streams one stripe");
   static_assert(AR == 16 || (AR == 8 && MT == 1 && !GROUPED), "8-row tiles: one plain tile");
   constexpr int kW = NT * 2048;                       // 16 * NT weight rows x 128 B
-  constexpr int kCap = wide_scale_cap(MT);
+  constexpr int kCap = wide_scale_cap();
   constexpr int kOffSa = MT * AR * 128;               // in an activation slot (no PRE)
   constexpr int kOffSb = kOffSa + 256;
   constexpr int kA = MT * AR * 128 + (PRE ? 0 : 512); // MT tiles (+ 64 sa + 64 sb)
@@ -1517,7 +1517,7 @@ struct CfgEntry {
   KernelFn fn[3];  // [out_dt index]
   // tiled (kind 2) and persistent (kind 3): the grouped-expert variant, where
   // built (else null); wide decode (kind 4): the variant without the scale
-  // preload, for more than wide_scale_cap(MT) groups per wave
+  // preload, for more than wide_scale_cap() groups per wave
   KernelFn fn_alt[3];
   // wide decode (kind 4): the grouped-expert variants with and without the
   // scale preload, where built (else null)
@@ -1940,7 +1940,7 @@ int gemm_block(void* c, const uint8_t* a_q, const float* a_scales, const uint8_t
     // one workgroup per bn-row weight stripe group and 16*MT activation rows
     // over the whole K range, or over one of split_k K ranges (grid z, split-K
     // fixup); stripe and tile rows are addressed with 32-bit offsets.  The
-    // scale preload holds wide_scale_cap(MT) groups per wave; a longer range
+    // scale preload holds wide_scale_cap() groups per wave; a longer range
     // per wave takes the kernel without it.
     if ((int64_t)cf.bm * k > 0x7FFFFFFF || (int64_t)cf.bn * k > 0x7FFFFFFF)
       return hipErrorInvalidValue;
@@ -1953,7 +1953,7 @@ int gemm_block(void* c, const uint8_t* a_q, const float* a_scales, const uint8_t
       if (e != hipSuccess) return e;
     }
     const int64_t per_wave = ((kg + split - 1) / split + cf.waves - 1) / cf.waves;
-    const KernelFn fn = per_wave <= wide_scale_cap(cf.bm / 16) ? cf.fn[di] : cf.fn_alt[di];
+    const KernelFn fn = per_wave <= wide_scale_cap() ? cf.fn[di] : cf.fn_alt[di];
     hipLaunchKernelGGL(fn, dim3((unsigned)tn, (unsigned)tm, (unsigned)split), dim3(64 * cf.waves),
                        0, st, args);
   } else if (cf.kind == 3) {
@@ -2057,7 +2057,7 @@ extern "C" int inferop_hip_gemm_w8a8_block_grouped(void* c, const uint8_t* a_q,
     // one workgroup per (16-row weight stripe, virtual M tile of the experts)
     if (16 * k > 0x7FFFFFFF || tmv > 65535) return hipErrorInvalidConfiguration;
     const int64_t per_wave = (k / 128 + cf.waves - 1) / cf.waves;
-    const KernelFn fn = per_wave <= wide_scale_cap(cf.bm / 16) ? cf.fn_grp[di] : cf.fn_grp_alt[di];
+    const KernelFn fn = per_wave <= wide_scale_cap() ? cf.fn_grp[di] : cf.fn_grp_alt[di];
     hipLaunchKernelGGL(fn, dim3((unsigned)tn, (unsigned)tmv), dim3(64 * cf.waves), 0, st, args);
     return hipGetLastError();
   }

@@ -122,8 +122,9 @@ int inferop_hip_diag_mfma_loop(int32_t iters, int32_t blocks, int32_t promote, u
                                void* stream);
 /* stripe_read: one read of the [n, k] byte matrix b by one 8-wave workgroup
  * per 16-row stripe, all of a workgroup's loads in flight, in access pattern
- * 0-3 (8-row register loads, contiguous register loads, MFMA-layout register
- * loads, 8-row direct-to-LDS loads); stripes > 0 makes workgroup i read
+ * 0-4 (8-row register loads, contiguous register loads, MFMA-layout register
+ * loads, 8-row direct-to-LDS loads, 8-row register loads written to LDS);
+ * stripes > 0 makes workgroup i read
  * stripe i % stripes (L2-resident).  n % 16 == 0, k / 1024 in {2, 7, 8}. */
 int inferop_hip_diag_stripe_read(const void* b, int64_t n, int64_t k, int32_t pattern,
                                  int32_t stripes, uint32_t* sink, void* stream);

@@ -132,7 +132,7 @@ int inferop_hip_diag_read_stream(const void*, int64_t bytes, int32_t blocks, uin
 int inferop_hip_diag_stripe_read(const void*, int64_t n, int64_t k, int32_t pattern,
                                  int32_t stripes, uint32_t*, void*) {
   check(n >= 16 && n % 16 == 0 && (k == 2048 || k == 7168 || k == 8192) && pattern >= 0 &&
-            pattern <= 3 && stripes >= 0 && stripes <= n / 16,
+            pattern <= 4 && stripes >= 0 && stripes <= n / 16,
         "stripe read args");
   return 0;
 }
@@ -225,7 +225,7 @@ void host_layer() {
         "stripe read k");
   check(inferop_diag_stripe_read(d, 100, 2048, 0, 0, d, nullptr) == INFEROP_ERR_ARGUMENT,
         "stripe read n");
-  check(inferop_diag_stripe_read(d, 4096, 7168, 4, 0, d, nullptr) == INFEROP_ERR_ARGUMENT,
+  check(inferop_diag_stripe_read(d, 4096, 7168, 5, 0, d, nullptr) == INFEROP_ERR_ARGUMENT,
         "stripe read pattern");
   check(inferop_diag_stripe_read(d, 4096, 7168, 3, 16, d, nullptr) == INFEROP_OK,
         "stripe read resident");

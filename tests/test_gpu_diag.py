@@ -16,7 +16,7 @@ def test_stripe_read_patterns_launch():
     sink = torch.zeros(4, dtype=torch.int32, device=dev)
     for (n, k) in ((4096, 7168), (2112, 7168), (7168, 2048)):
         b = torch.randint(0, 255, (n, k), dtype=torch.uint8, device=dev)
-        for pattern in range(4):
+        for pattern in range(5):
             for stripes in (0, 16):
                 print(f"stripe read n={n} k={k} pattern={pattern} stripes={stripes}", flush=True)
                 assert inferop_amd.diag_stripe_read(b, n, k, pattern, stripes, sink) == S.OK
@@ -24,7 +24,7 @@ def test_stripe_read_patterns_launch():
     b = torch.zeros((64, 2048), dtype=torch.uint8, device=dev)
     assert inferop_amd.diag_stripe_read(b, 64, 3072, 0, 0, sink) == S.ERR_ARGUMENT
     assert inferop_amd.diag_stripe_read(b, 60, 2048, 0, 0, sink) == S.ERR_ARGUMENT
-    assert inferop_amd.diag_stripe_read(b, 64, 2048, 4, 0, sink) == S.ERR_ARGUMENT
+    assert inferop_amd.diag_stripe_read(b, 64, 2048, 5, 0, sink) == S.ERR_ARGUMENT
     assert inferop_amd.diag_stripe_read(b, 64, 2048, 0, 5, sink) == S.ERR_ARGUMENT
     torch.cuda.synchronize()
     assert int(sink[0]) == 0 or int(sink[0]) == int(0x9E3779B9 - (1 << 32))
