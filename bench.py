@@ -60,7 +60,7 @@ PREFILL_LAUNCHES = 20
 # WRITE_SIZE from rocprofv3 runs of `bench.py --traffic-pass`, each scaled by
 # what the counter reads for a 256 MiB streaming kernel in the same process
 # (per-launch table and commands: profiles/decode_step_hbm_traffic.md).
-DECODE_GEMM_TRAFFIC_BYTES = 22134721
+DECODE_GEMM_TRAFFIC_BYTES = 22147667
 
 
 def quant_bytes(m, k, in_bytes=2):
