@@ -58,6 +58,18 @@ __device__ __forceinline__ f32x2 cvt_pk2_e4m3_f32(uint32_t w) {
 // ---- output conversions ---------------------------------------------------------
 // bf16 / fp16 stores round to nearest-even (v_cvt_pk_bf16_f32, v_cvt_f16_f32),
 // the conversions the reference's kernels use (__float2bfloat16, __float2half).
+
+// x as an fp32 register the optimiser cannot see through.  Narrowing an fp32
+// product to fp16 is otherwise folded into one mixed-precision FMA
+// (v_fma_mixlo_f16 a, b, 0), which rounds the exact product to fp16 once;
+// the C semantics, and the reference, round it to fp32 first, and the two
+// differ where the fp32 rounding lands on an fp16 tie.  Every fp32 -> fp16
+// conversion of a computed value goes through this.
+__device__ __forceinline__ float fp32_value(float x) {
+  asm("" : "+v"(x));
+  return x;
+}
+__device__ __forceinline__ _Float16 to_fp16(float x) { return (_Float16)fp32_value(x); }
 template <int OUT_DT>
 struct OutT;
 template <>
@@ -83,13 +95,16 @@ __device__ __forceinline__ void store4(void* dst, float a, float b, float c, flo
     *reinterpret_cast<bf16x4*>(dst) = bf16x4{(__bf16)a, (__bf16)b, (__bf16)c, (__bf16)d};
   } else {
     typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-    *reinterpret_cast<f16x4*>(dst) = f16x4{(_Float16)a, (_Float16)b, (_Float16)c, (_Float16)d};
+    *reinterpret_cast<f16x4*>(dst) = f16x4{to_fp16(a), to_fp16(b), to_fp16(c), to_fp16(d)};
   }
 }
 
 template <int OUT_DT>
 __device__ __forceinline__ void store1(void* dst, float a) {
-  *reinterpret_cast<typename OutT<OUT_DT>::T*>(dst) = (typename OutT<OUT_DT>::T)a;
+  if constexpr (OUT_DT == kFp16)
+    *reinterpret_cast<_Float16*>(dst) = to_fp16(a);
+  else
+    *reinterpret_cast<typename OutT<OUT_DT>::T*>(dst) = (typename OutT<OUT_DT>::T)a;
 }
 
 }  // namespace inferop_hip

@@ -150,3 +150,63 @@ def test_dequant_parity(out, gs):
     # fp32: bit-exact; 16-bit: the oracle's fp32 value rounded to nearest-even
     want_t = torch.from_numpy(want).to(xd.dtype).float().numpy()
     assert np.array_equal(got.view(np.uint32), want_t.view(np.uint32))
+
+
+def _e4m3_value(b: int) -> float:
+    e, m = (b >> 3) & 15, b & 7
+    v = m / 8 * 2.0 ** -6 if e == 0 else (1 + m / 8) * 2.0 ** (e - 7)
+    return -v if b & 0x80 else v
+
+
+def _fp16_tie_cases():
+    """(e4m3 byte, fp32 scale) pairs whose exact product lies just below an
+    fp16 rounding midpoint and rounds to it in fp32: rounding the fp32 product
+    to fp16 (ties to even, upwards here) differs from rounding the exact
+    product to fp16 once (downwards)."""
+    rng = np.random.default_rng(5)
+    cases = []
+    for b in range(1, 0x7F):
+        qv = _e4m3_value(b)
+        for _ in range(200):
+            e, j = int(rng.integers(-8, 12)), int(rng.integers(1024, 2048)) | 1
+            mid = (2 * j + 1) * 2.0 ** (e - 11)  # between odd j and even j + 1 (x 2^(e-10))
+            s0 = np.float32(mid / qv)
+            hit = None
+            for d in range(-3, 4):
+                sc = np.float32(s0 + np.float32(d) * np.spacing(s0))
+                exact = qv * float(sc)  # 4 x 24 significant bits: exact in fp64
+                if np.float16(np.float32(exact)).view(np.uint16) != np.float16(exact).view(np.uint16):
+                    hit = sc
+                    break
+            if hit is not None:
+                cases.append((b, hit))
+                break
+    return cases
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("gs", [128, 64, 48, 40])
+def test_dequant_fp16_rounds_through_fp32(gs):
+    """fp16 output is the fp32 product rounded to fp16 (two roundings, as in
+    the reference), not the exact product rounded once: every group here is
+    a case where the two differ."""
+    device()
+    cases = _fp16_tie_cases()
+    assert len(cases) > 64
+    m, k = 16, gs * 8
+    q = np.empty((m, k), np.uint8)
+    s = np.empty((m, k // gs), np.float32)
+    for r in range(m):
+        for c in range(k // gs):
+            b, sc = cases[(r * (k // gs) + c) % len(cases)]
+            q[r, c * gs:(c + 1) * gs] = b | (0x80 if (r + c) % 2 else 0)
+            s[r, c] = sc
+    want = torch.from_numpy(oracle.dequant(q, s, gs)).to(torch.float16).numpy()
+    once = np.array([[_e4m3_value(int(q[r, j])) * float(s[r, j // gs]) for j in range(k)]
+                     for r in range(m)]).astype(np.float16)
+    assert not np.any(once.view(np.uint16) == want.view(np.uint16))
+    xd = torch.empty((m, k), dtype=torch.float16, device="cuda:0")
+    assert inferop_amd.dequant_fp8_per_token_group(xd, DT.fp16, to_dev(q), to_dev(s), m, k,
+                                                   gs) == 0
+    got = xd.cpu().numpy()
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
