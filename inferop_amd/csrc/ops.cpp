@@ -199,6 +199,15 @@ GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
     const int64_t tiles = ((n + 63) / 64) * ((m + 63) / 64);
     return {kPreN64M64S4, int32_t(kg >= 32 ? small_tile_split(tiles) : 1)};
   }
+  if (m > 64 && m <= 128 && !huge_k && kg >= 48 && (n + 255) / 256 <= cus) {
+    // More 128x128 tiles than CUs, but the 256x128 tiles (all M rows with 256
+    // weight rows) fit in one round: a CU then reads the activations once per
+    // 256 weight rows instead of once per 128, and no partial second round
+    // follows.  Same box, K=7168: M=128, N=36864 96.6 -> 89.3 us, N=33280
+    // 95.1 -> 88.9 us, M=96 92.7 -> 88.6 us; for K <= 4096 the 128x128 tiles
+    // stay ahead by about 2%.
+    return {kPreN256M128S3, 1};
+  }
   if (m <= 16 && !huge_k) {
     // HBM-bound: a workgroup owns 16 weight rows over the whole K range on
     // the wide decode kernel.  A long K over stripes for fewer than half the

@@ -201,6 +201,11 @@ def test_gemm_selection_covers_configs():
     assert sel(64, 36864, 7168) == ("pre_n128_m64_w8_s4", 2)
     assert sel(128, 7168, 2048) == ("dw_n64_m64_k4_w2a2", 1)
     assert sel(128, 4096, 512) == ("dw_n64_m32_k4_w2a2", 1)
+    assert sel(128, 7168, 18432) == ("per_n128_m128_w4", 4)
+    # more 128x128 tiles than CUs at M <= 128: one round of 256x128 tiles
+    assert sel(128, 36864, 7168) == ("pre_n256_m128_w8_s3", 1)
+    assert sel(96, 36864, 7168) == ("pre_n256_m128_w8_s3", 1)
+    assert sel(128, 40960, 4096)[0] != "pre_n256_m128_w8_s3"
     # 256x256 prefill tiles run on the persistent kernel when K / 128 is even,
     # on the one-tile-per-workgroup kernel otherwise
     assert names[inferop_amd.gemm_select(4096, 7168, 16384)[0]] == "per_n256_m256_w8"
