@@ -1168,7 +1168,17 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_persist_kernel(GemmArgs a) 
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wn = wave % WN, wm = wave / WN;
+  // Grouped tiles with two waves per SIMD: wave rows from the bottom of the
+  // tile up, so that in an expert's last tile, which often ends early, the
+  // waves with no rows left are the loading ones (0 .. NL-1); they skip the
+  // multiply and only issue loads, and the busy wave on each SIMD has the
+  // matrix core to itself (32 experts, N=4096, K=7168, 4096 rows on 256x256
+  // tiles: 270.7 -> 250 us; 2048 rows 242 -> 220 us).  With one wave per
+  // SIMD (128x128 tiles) nothing is gained and it measured 4% slower; the
+  // plain GEMM keeps top-down rows (the reversed order spills 64 more
+  // registers there).
+  constexpr bool kSkipIdle = GROUPED && NW >= 8;
+  const int wn = wave % WN, wm = kSkipIdle ? WM - 1 - wave / WN : wave / WN;
   const int M = a.m, N = a.n, K = a.k;
   const int KG = K >> 7;
   const int NB = (N + 127) >> 7;
@@ -1369,22 +1379,34 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_persist_kernel(GemmArgs a) 
       for (int i = 0; i < SN; ++i)
 #pragma unroll
         for (int j = 0; j < SM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      // (kSkipIdle) a wave whose rows all lie past the tile's last row
+      // multiplies nothing: its accumulators stay zero and its rows are never
+      // stored; it still issues its share of the loads.
+      const bool busy = !kSkipIdle || m0 + wm * TM < mend;
+      auto step = [&](const uint8_t* st, auto between) {
+        if (busy) {
+          compute(st, between);
+        } else {
+#pragma unroll
+          for (int i = 0; i < SN; ++i) between(i);
+        }
+      };
       // on entry group gb of the unit is in buffer 0 (gb and ge are even)
       for (int g0 = gb; g0 + 2 < ge; g0 += 2) {
-        compute(smem0, spread(g0 + 1, smem1));
+        step(smem0, spread(g0 + 1, smem1));
         pin_acc();
         barrier();  // group g0 + 1 landed; every wave is done with buffer 0
-        compute(smem1, spread(g0 + 2, smem0));
+        step(smem1, spread(g0 + 2, smem0));
         pin_acc();
         barrier();  // group g0 + 2 landed; every wave is done with buffer 1
       }
-      compute(smem0, spread(ge - 1, smem1));
+      step(smem0, spread(ge - 1, smem1));
       pin_acc();
       barrier();  // group ge - 1 landed; every wave is done with buffer 0
       // the next unit's first group (the last unit reloads its own, which
       // keeps the group free of branches)
       set_loads(nn0, nm0, nmend, nex);
-      compute(smem1, spread(ngb, smem0));
+      step(smem1, spread(ngb, smem0));
       pin_acc();
       barrier();  // the next unit's first group landed; buffer 1 is free
 
