@@ -328,7 +328,7 @@ hipError_t launch_dequant(void* x, const uint8_t* q, const float* scales, int64_
 // tests/test_gemm.cpp:28-45): per block, absmax over its rows (ignoring NaN),
 // scale = absmax == 0 ? 1 : absmax * fl32(1/448), inv = 1 / scale (IEEE), and
 // q = e4m3_rn_sat(w * inv) -- a product with the reciprocal, not a quotient.
-// Thread t owns 8 consecutive columns (t % 16) of rows t / 16 + 16 i.  Blocks
+// Thread t owns 8 columns (slot t % 16) of rows t / 16 + 16 i.  Blocks
 // whose absmax is Inf/NaN or below 2^-80 take the slow path (software encoder,
 // x86-64 NaN results, as in the per-token quantizer); elsewhere |w * inv| <=
 // 448 and products are never subnormal, so the hardware multiply and encode
@@ -362,7 +362,12 @@ __global__ __launch_bounds__(256) void weight_block_quant_kernel(uint8_t* __rest
   const int c = t & 15;
   const int64_t kg = k >> 7;
   const int64_t g = blockIdx.x, nb = blockIdx.y;
-  const int64_t col = g * 128 + c * 8;
+  // columns of thread t: 16-bit inputs 8 consecutive ones (16 bytes, so 16
+  // lanes read a row's 256 bytes with one instruction); fp32 inputs two runs
+  // of 4, at c * 4 and 64 + c * 4, so each of the two 16-byte loads of a row
+  // covers 256 contiguous bytes (rather than half of every 32 bytes)
+  const int64_t col = g * 128 + c * (DT == kFp32 ? 4 : 8);
+  constexpr int64_t kHiCol = DT == kFp32 ? 64 : 4;  // offset of columns 4..7
   // the block's values stay in registers as loaded (16-bit inputs packed two
   // to a word: half the registers of fp32 copies, so more workgroups per CU)
   constexpr int W = DT == kFp32 ? 8 : 4;
@@ -377,6 +382,15 @@ __global__ __launch_bounds__(256) void weight_block_quant_kernel(uint8_t* __rest
           _Float16, (uint16_t)((j & 1) ? (wv[i][j >> 1] >> 16) : (wv[i][j >> 1] & 0xFFFFu)));
     }
   };
+  // the codes of the thread's columns 0..3 (lo) and 4..7 (hi) of a row
+  auto store_codes = [&](uint8_t* dst, uint32_t lo, uint32_t hi) {
+    if constexpr (DT == kFp32) {
+      *reinterpret_cast<uint32_t*>(dst) = lo;
+      *reinterpret_cast<uint32_t*>(dst + kHiCol) = hi;
+    } else {
+      *reinterpret_cast<u32x2*>(dst) = u32x2{lo, hi};
+    }
+  };
   uint32_t key = 0;
 #pragma unroll
   for (int i = 0; i < kRows; ++i) {
@@ -384,8 +398,9 @@ __global__ __launch_bounds__(256) void weight_block_quant_kernel(uint8_t* __rest
     if (row < n) {
       const int64_t e = row * k + col;
       if constexpr (DT == kFp32) {
-        const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(w) + e);
-        const u32x4 a = p[0], b = p[1];
+        const float* p = reinterpret_cast<const float*>(w) + e;
+        const u32x4 a = *reinterpret_cast<const u32x4*>(p);
+        const u32x4 b = *reinterpret_cast<const u32x4*>(p + kHiCol);
         wv[i][0] = a.x, wv[i][1] = a.y, wv[i][2] = a.z, wv[i][3] = a.w;
         wv[i][4] = b.x, wv[i][5] = b.y, wv[i][6] = b.z, wv[i][7] = b.w;
       } else {
@@ -418,7 +433,7 @@ __global__ __launch_bounds__(256) void weight_block_quant_kernel(uint8_t* __rest
       if (row < n) {
         const uint32_t lo = cvt_pk4_e4m3(val(i, 0) * inv, val(i, 1) * inv, val(i, 2) * inv, val(i, 3) * inv);
         const uint32_t hi = cvt_pk4_e4m3(val(i, 4) * inv, val(i, 5) * inv, val(i, 6) * inv, val(i, 7) * inv);
-        *reinterpret_cast<u32x2*>(q + row * k + col) = u32x2{lo, hi};
+        store_codes(q + row * k + col, lo, hi);
       }
     }
   } else {
@@ -433,8 +448,9 @@ __global__ __launch_bounds__(256) void weight_block_quant_kernel(uint8_t* __rest
       }
       const int64_t e = row * k + col;
       if constexpr (DT == kFp32) {
-        const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(w) + e);
-        const u32x4 a = p[0], b = p[1];
+        const float* p = reinterpret_cast<const float*>(w) + e;
+        const u32x4 a = *reinterpret_cast<const u32x4*>(p);
+        const u32x4 b = *reinterpret_cast<const u32x4*>(p + kHiCol);
         const uint32_t r[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
         for (int j = 0; j < 8; ++j) x[j] = u2f(r[j]);
@@ -473,9 +489,8 @@ __global__ __launch_bounds__(256) void weight_block_quant_kernel(uint8_t* __rest
         uint32_t cd[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) cd[j] = slow_code_mul(x[j], inv);
-        *reinterpret_cast<u32x2*>(q + row * k + col) =
-            u32x2{cd[0] | (cd[1] << 8) | (cd[2] << 16) | (cd[3] << 24),
-                  cd[4] | (cd[5] << 8) | (cd[6] << 16) | (cd[7] << 24)};
+        store_codes(q + row * k + col, cd[0] | (cd[1] << 8) | (cd[2] << 16) | (cd[3] << 24),
+                    cd[4] | (cd[5] << 8) | (cd[6] << 16) | (cd[7] << 24));
       }
     }
   }
