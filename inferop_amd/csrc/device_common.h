@@ -85,6 +85,15 @@ struct OutT<kBf16> {
   using T = __bf16;
 };
 
+// An fp32 result as the output type (fp16 through to_fp16).
+template <int OUT_DT>
+__device__ __forceinline__ typename OutT<OUT_DT>::T to_out(float x) {
+  if constexpr (OUT_DT == kFp16)
+    return to_fp16(x);
+  else
+    return (typename OutT<OUT_DT>::T)x;
+}
+
 // Store 4 consecutive outputs (row-major, 4-element aligned) as one vector.
 template <int OUT_DT>
 __device__ __forceinline__ void store4(void* dst, float a, float b, float c, float d) {

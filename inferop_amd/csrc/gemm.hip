@@ -1081,7 +1081,8 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_prefill_kernel(GemmArgs a) 
         const int ml = wm * TM + 16 * j + rsub, nl = wn * TN + 16 * i + 4 * c0;
         typedef OT ot4 __attribute__((ext_vector_type(4)));
         *reinterpret_cast<ot4*>(crow(ml) + nl * 2) =
-            ot4{(OT)acc[i][j][0], (OT)acc[i][j][1], (OT)acc[i][j][2], (OT)acc[i][j][3]};
+            ot4{to_out<OUT_DT>(acc[i][j][0]), to_out<OUT_DT>(acc[i][j][1]),
+                to_out<OUT_DT>(acc[i][j][2]), to_out<OUT_DT>(acc[i][j][3])};
       }
     stage_barrier<0>();
     constexpr int kChunks = BN / 8;  // 16-byte pieces per tile row
@@ -1444,7 +1445,8 @@ __global__ __launch_bounds__(64 * WN * WM) void gemm_persist_kernel(GemmArgs a) 
             } else {
               typedef OT ot4 __attribute__((ext_vector_type(4)));
               *reinterpret_cast<ot4*>(dst) =
-                  ot4{(OT)acc[i][j][0], (OT)acc[i][j][1], (OT)acc[i][j][2], (OT)acc[i][j][3]};
+                  ot4{to_out<OUT_DT>(acc[i][j][0]), to_out<OUT_DT>(acc[i][j][1]),
+                      to_out<OUT_DT>(acc[i][j][2]), to_out<OUT_DT>(acc[i][j][3])};
             }
           }
         }

@@ -64,6 +64,29 @@ def test_topk_ties_and_underflow():
         assert np.array_equal(w.view(np.uint32), w_r.view(np.uint32))
 
 
+def test_topk_ties_across_lanes_and_slots():
+    """256 experts (four per lane): equal maxima held by one lane, by several
+    lanes, and by several slots of one lane, so both ways the kernel picks
+    the lowest expert among equal probabilities are taken."""
+    device()
+    g = np.random.default_rng(77)
+    lg = np.round(g.standard_normal((40, 256))).astype(np.float32)  # many ties
+    lg[0] = 0.0                                   # every expert tied
+    lg[1] = -5.0
+    lg[1, [5, 69, 133, 197]] = 2.0                # one lane (5), all four slots
+    lg[2] = -5.0
+    lg[2, [200, 7, 130, 63]] = 2.0                # four lanes, different slots
+    lg[3] = -5.0
+    lg[3, 250] = 3.0                              # one holder, then a tie
+    lg[3, [64, 1]] = 2.0
+    for k, renorm in ((8, True), (8, False), (13, True)):
+        ids, w = _gpu(lg, k, renorm)
+        ids_r, w_r = oracle.topk_softmax(lg, k, renorm)
+        assert np.array_equal(ids, ids_r)
+        assert np.allclose(w, w_r, rtol=4 * 2.0 ** -24, atol=0)
+    assert list(ids_r[1, :4]) == [5, 69, 133, 197] and list(ids_r[2, :4]) == [7, 63, 130, 200]
+
+
 def test_topk_rejected_calls():
     device()
     S = ia.Status
