@@ -1,6 +1,10 @@
 """The FP8 path inside a captured HIP graph: every replay must reproduce the
 eager result bit for bit (split-K counters reset themselves inside the
 kernel; nothing in the path records a memset node)."""
+import os
+import subprocess
+import sys
+
 import numpy as np
 import pytest
 import torch
@@ -158,3 +162,95 @@ def test_graph_split_k_workspace_survives_larger_eager_calls():
             g.replay()
         st.synchronize()
         assert torch.equal(c_small, want_small), f"replay {rep}"
+
+
+_SILU_FIRST_CALL_CAPTURED = r"""
+import sys
+import torch
+import inferop_amd
+DT = inferop_amd.dtype
+tokens, d = 64, 2048
+g = torch.Generator(device="cuda:0").manual_seed(5)
+gu = (torch.randn((tokens, 2 * d), generator=g, device="cuda:0") * 3).to(torch.bfloat16)
+q = torch.empty((tokens, d), dtype=torch.uint8, device="cuda:0")
+s = torch.empty((tokens, d // 128), dtype=torch.float32, device="cuda:0")
+st = torch.cuda.Stream()
+graph = torch.cuda.CUDAGraph()
+# the process's first bf16 SiLU call, inside the capture: the library builds
+# its SiLU table on its own stream in relaxed capture mode
+with torch.cuda.graph(graph, stream=st):
+    assert inferop_amd.silu_and_mul_quant_fp8(q, s, gu, DT.bf16, tokens, d,
+                                              stream=st.cuda_stream) == 0
+q2, s2 = torch.empty_like(q), torch.empty_like(s)
+with torch.cuda.stream(st):
+    assert inferop_amd.silu_and_mul_quant_fp8(q2, s2, gu, DT.bf16, tokens, d,
+                                              stream=st.cuda_stream) == 0
+st.synchronize()
+for rep in range(3):
+    q.zero_(); s.zero_(); torch.cuda.synchronize()
+    graph.replay(); torch.cuda.synchronize()
+    if not (torch.equal(q, q2) and torch.equal(s, s2)):
+        print("replay", rep, "differs from eager", flush=True)
+        sys.exit(1)
+print("ok", flush=True)
+"""
+
+
+@pytest.mark.gpu
+def test_graph_silu_first_call_captured_in_fresh_process():
+    # a child process, so that the captured call is its first bf16 SiLU call
+    device()
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, PYTHONPATH=root + os.pathsep + os.environ.get("PYTHONPATH", ""))
+    r = subprocess.run([sys.executable, "-c", _SILU_FIRST_CALL_CAPTURED], env=env,
+                       capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0 and "ok" in r.stdout, (r.stdout[-2000:], r.stderr[-2000:])
+
+
+@pytest.mark.gpu
+def test_graph_fused_producers_replay_match_eager():
+    device()
+    tokens, d, rows, cols = 48, 4096, 40, 2048
+    g = torch.Generator(device="cuda:0").manual_seed(9)
+    gu = (torch.randn((tokens, 2 * d), generator=g, device="cuda:0") * 3).to(torch.bfloat16)
+    x = torch.randn((rows, cols), generator=g, device="cuda:0").to(torch.bfloat16)
+    w = torch.randn((cols,), generator=g, device="cuda:0").to(torch.bfloat16)
+    res0 = torch.randn((rows, cols), generator=g, device="cuda:0").to(torch.bfloat16)
+    st = torch.cuda.Stream()
+    outs = {}
+
+    def run(tag):
+        q = torch.empty((tokens, d), dtype=torch.uint8, device="cuda:0")
+        s = torch.empty((tokens, d // 128), dtype=torch.float32, device="cuda:0")
+        res = res0.clone()
+        rq = torch.empty((rows, cols), dtype=torch.uint8, device="cuda:0")
+        rs = torch.empty((rows, cols // 128), dtype=torch.float32, device="cuda:0")
+        outs[tag] = (q, s, res, rq, rs)
+
+    run("eager")
+    run("graph")
+
+    def call(tag):
+        q, s, res, rq, rs = outs[tag]
+        assert inferop_amd.silu_and_mul_quant_fp8(q, s, gu, DT.bf16, tokens, d,
+                                                  stream=st.cuda_stream) == 0
+        assert inferop_amd.fused_add_rmsnorm_quant_fp8(res, rq, rs, x, w, DT.bf16, rows, cols,
+                                                       stream=st.cuda_stream) == 0
+
+    with torch.cuda.stream(st):
+        call("eager")
+    st.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        call("graph")
+    for rep in range(3):
+        q, s, res, rq, rs = outs["graph"]
+        q.zero_()
+        s.zero_()
+        rq.zero_()
+        res.copy_(res0)  # the residual is updated in place
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(outs["graph"], outs["eager"]):
+            assert torch.equal(a, b), f"replay {rep}"
