@@ -179,6 +179,21 @@ GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
     return {kPreN128M64S4, int32_t(split < 1 ? 1 : split)};
   }
   if (m > 64 && m <= 128 && !huge_k && ((n + 127) / 128) * ((m + 127) / 128) < cus) {
+    // Multi-stripe wide decode tiles (64 weight rows x 64 activation rows,
+    // the two activation tiles of a row group on one XCD) when they fill
+    // three quarters of the CUs in one round below 64 scale groups, or split
+    // K at least twice from 64 groups up (a CU then reads no more than on the
+    // persistent 128x128 tiles with their 4-way tail split).  Same box, us:
+    // M=100, N=4096, K=7168 17.0 -> 15.3; M=128: N=4096, K=7168 20.0 -> 15.5;
+    // N=7168, K=4096 20.3 -> 15.9; N=2048, K=4096 14.4 -> 10.2; N=4096,
+    // K=16384 41.4 -> 29.2; M=96, N=7168, K=7168 25.6 -> 22.4.  Not taken:
+    // M=72, N=4608 (144 workgroups: 21.5 against 17.7) and M=128, N=7168,
+    // K=18432 (one split: 61.0 against 50.9).
+    if (tx64 % 8 == 0) {
+      const int64_t wgs = tx64 * ((m + 63) / 64);
+      const int32_t s = nt_split(wgs);
+      if (kg >= 64 ? s >= 2 : 4 * wgs * s >= 3 * (int64_t)cus) return {kDwN64M64, s};
+    }
     // Still HBM-bound and too few 128x128 tiles to occupy every CU.  A long K
     // (64 scale groups or more): 128x64 tiles, three stages, K split so about
     // two workgroups run per CU (M=128, N=7168, K=18432: 57 us against 67 us

@@ -206,6 +206,14 @@ def test_gemm_selection_covers_configs():
     assert sel(128, 36864, 7168) == ("pre_n256_m128_w8_s3", 1)
     assert sel(96, 36864, 7168) == ("pre_n256_m128_w8_s3", 1)
     assert sel(128, 40960, 4096)[0] != "pre_n256_m128_w8_s3"
+    # M in (64, 128], fewer 128x128 tiles than CUs, 64-row groups a multiple
+    # of 8: 64x64 wide decode tiles when they fill the CUs
+    assert sel(100, 4096, 7168) == ("dw_n64_m64_k4_w2a2", 2)
+    assert sel(96, 7168, 7168) == ("dw_n64_m64_k4_w2a2", 1)
+    assert sel(128, 2048, 4096) == ("dw_n64_m64_k4_w2a2", 4)
+    assert sel(128, 4096, 16384) == ("dw_n64_m64_k4_w2a2", 2)
+    assert sel(72, 4608, 7168)[0] == "pre_n64_m64_w4_s4"
+    assert sel(77, 4672, 7168)[0] == "pre_n64_m64_w4_s4"
     # 256x256 prefill tiles run on the persistent kernel when K / 128 is even,
     # on the one-tile-per-workgroup kernel otherwise
     assert names[inferop_amd.gemm_select(4096, 7168, 16384)[0]] == "per_n256_m256_w8"
