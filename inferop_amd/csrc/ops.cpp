@@ -133,12 +133,73 @@ GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
     if (sp > kg / 8) sp = kg / 8;
     return int32_t(sp < 1 ? 1 : sp);
   };
+  // The 64-weight-row wide decode tiles from 65 to 512 rows: 32-row activation
+  // tiles, else 64-row ones, each when one round of them (K split as above)
+  // covers three quarters of the CUs.  From 96 scale groups up the K must be
+  // split at least twice (one workgroup streaming the whole K is slower than
+  // the persistent 128x128 tiles: M=128, N=7168, K=18432 61.0 us against 50.9;
+  // at K=8192, M=160, N=4096 unsplit 64-row tiles take 23.5 us, 64x64
+  // LDS-staged tiles 28.6), and unsplit 32-row tiles give way to 64-row tiles
+  // that fill the CUs (M=96, N=4096, K=7168: 16.1 us against 15.7 in two;
+  // M=224, N=2048, K=10240 22.8 against 18.6), except up to 32 scale groups,
+  // where the split's partial round trip costs more than idle CUs and unsplit
+  // 32-row tiles filling five eighths of them win (M=144, N=2048, K=4096: 10.0
+  // us against 11.2 on 64-row tiles in two).  Every XCD reads all activation
+  // rows, so M x K must fit its 4 MB L2 (M=448, N=2048, K=10240: 33.8 us
+  // against 27.1 on 64x64 LDS-staged tiles).  Weight row groups that are not a
+  // multiple of 8 put the activation tiles of a row group on different XCDs,
+  // each reading the rows from HBM: then only a small weight (N <= 1024) over
+  // at most six 32-row tiles, two thirds of the CUs busy (M=96, N=576, K=7168:
+  // 8.9 us against 13.9 on 64x64 LDS-staged tiles).
+  auto wide_tiles = [&](GemmChoice* ch) {
+    if (kg < 8 || m * k > (int64_t(4) << 20)) return false;
+    const bool aligned = tx64 % 8 == 0;
+    if (!aligned && !(n <= 1024 && m <= 192)) return false;
+    const int64_t w32 = tx64 * ((m + 31) / 32), w64 = tx64 * ((m + 63) / 64);
+    const int32_t s32 = nt_split(w32), s64 = nt_split(w64);
+    const int64_t c = cus;
+    const bool fill32 = w32 <= c && (kg < 96 || s32 >= 2) &&
+                        (!aligned   ? 3 * w32 * s32 >= 2 * c
+                         : kg <= 32 ? 8 * w32 * s32 >= 5 * c
+                                    : 4 * w32 * s32 >= 3 * c);
+    const bool fill64 = aligned && w64 <= c && (kg >= 96 ? s64 >= 2 : 4 * w64 * s64 >= 3 * c);
+    if (fill32 && (s32 >= 2 || kg <= 32 || !fill64)) {
+      *ch = {kDwN64M32, s32};
+      return true;
+    }
+    if (fill64) {
+      *ch = {kDwN64M64, s64};
+      return true;
+    }
+    return false;
+  };
+  // K split of the 64x64 LDS-staged tiles: unsplit below 32 scale groups,
+  // else the split that keeps them to one round of two per CU, at most 6
+  // (M=96, N=576, K=7168: 14 splits 13.9 us, 6 splits 11.4) and with the
+  // fp32 partials of all splits, 4 * split * M bytes a column, no more than
+  // the K bytes of weight a column (M=384, N=576, K=7168: 4 splits 13.6 us,
+  // 6 splits 14.5).
+  auto lds64_split = [&](int64_t t64) {
+    if (kg < 32) return int32_t(1);
+    int64_t split = small_tile_split(t64);
+    if (split > 6) split = 6;
+    if (4 * split * m > k) split = k / (4 * m);
+    return int32_t(split < 1 ? 1 : split);
+  };
   if (m > 32 && m <= 64 && !huge_k) {
     // one round of workgroups at most (one per CU); M=64, K=7168: N=4096
     // 14.0 -> 12.3 us (64x32 tiles, split 2), N=2112 12.3 -> 10.3 us (32x64,
-    // split 3); K=2048, N=7168: 8.8 -> 7.4 us
-    if (tx64 % 8 == 0 && tx64 * ((m + 31) / 32) <= cus)
-      return {kDwN64M32, nt_split(tx64 * ((m + 31) / 32))};
+    // split 3); K=2048, N=7168: 8.8 -> 7.4 us.  From 64 scale groups up only
+    // with K split (M=48, N=7168, K=18432: 49.6 us unsplit, 35.5 on 128x64
+    // LDS-staged tiles in four)
+    // Up to 48 rows one 64-row activation tile (32x64 tiles) rather than
+    // two 32-row tiles, the second not half full (M=40, N=4096, K=7168: 13.2
+    // -> 11.5 us; N=7168, K=4096 12.1 -> 10.5).
+    const int64_t w32 = tx64 * ((m + 31) / 32);
+    if (m <= 48 && tx32 <= cus && (kg < 64 || nt_split(tx32) >= 2))
+      return {kDwN32M64, nt_split(tx32)};
+    if (tx64 % 8 == 0 && w32 <= cus && (kg < 64 || nt_split(w32) >= 2))
+      return {kDwN64M32, nt_split(w32)};
     if (tx64 % 8 != 0 && tx32 <= cus) return {kDwN32M64, nt_split(tx32)};
   }
   if (m > 64 && m <= 128 && !huge_k && kg <= 16 && tx64 % 8 == 0) {
@@ -153,7 +214,17 @@ GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
     // split-K); the activations, which every stripe reads again from L2, are
     // what limits it, so it serves up to about one stripe per CU for a long K
     // and two for K <= 4096 (the configurations fit two workgroups per CU).
-    if (m <= 32) return {kDwM32K4, 1};
+    if (m <= 32) {
+      // 17 to 32 rows, from 32 scale groups up: 64x32 wide decode tiles, K
+      // split to fill one round (M=24, K=7168: N=4096 11.6 -> 10.4 us, N=4608
+      // 15.7 -> 11.2, N=36864 65.9 -> 55.1; N=7168, K=18432 46.0 -> 28.1).
+      // Below that the stripe kernel, or 64x64 LDS-staged tiles beyond two
+      // stripes per CU (N=24576, K=1536 15.0 -> 12.0; N=32768, K=512 11.3 ->
+      // 6.8).
+      if (kg >= 32) return {kDwN64M32, nt_split(tx64)};
+      if (stripes > 2 * cus) return {kPreN64M64S4, 1};
+      return {kDwM32K4, 1};
+    }
     if (stripes <= cus && kg >= 32) {
       // with a quarter of the CUs or more left without a stripe, 128x32
       // tiles with K split across all CUs do better
@@ -189,11 +260,10 @@ GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
     // K=16384 41.4 -> 29.2; M=96, N=7168, K=7168 25.6 -> 22.4.  Not taken:
     // M=72, N=4608 (144 workgroups: 21.5 against 17.7) and M=128, N=7168,
     // K=18432 (one split: 61.0 against 50.9).
-    if (tx64 % 8 == 0) {
-      const int64_t wgs = tx64 * ((m + 63) / 64);
-      const int32_t s = nt_split(wgs);
-      if (kg >= 64 ? s >= 2 : 4 * wgs * s >= 3 * (int64_t)cus) return {kDwN64M64, s};
-    }
+    // (and 32-row activation tiles where they fill the CUs: M=72, N=4608,
+    // K=7168 17.9 -> 16.3 us; M=96, N=1536 11.8 -> 9.9; N=1024 11.7 -> 8.9)
+    GemmChoice wc;
+    if (wide_tiles(&wc)) return wc;
     // Still HBM-bound and too few 128x128 tiles to occupy every CU.  A long K
     // (64 scale groups or more): 128x64 tiles, three stages, K split so about
     // two workgroups run per CU (M=128, N=7168, K=18432: 57 us against 67 us
@@ -211,10 +281,13 @@ GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
       if (split > kg / 16) split = kg / 16;
       return {kPreN128M64S3, int32_t(split < 1 ? 1 : split)};
     }
+    // (the 64x64 tiles in one round of two per CU; beyond that the 128x128
+    // tiles below: M=96, N=24576, K=1536 15.9 us)
     const int64_t tiles = ((n + 63) / 64) * ((m + 63) / 64);
-    return {kPreN64M64S4, int32_t(kg >= 32 ? small_tile_split(tiles) : 1)};
+    if (tiles <= 2 * cus) return {kPreN64M64S4, lds64_split(tiles)};
   }
-  if (m > 64 && m <= 128 && !huge_k && kg >= 48 && (n + 255) / 256 <= cus) {
+  if (m > 64 && m <= 128 && !huge_k && kg >= 48 && (n + 255) / 256 <= cus &&
+      ((n + 127) / 128) * ((m + 127) / 128) >= cus) {
     // More 128x128 tiles than CUs, but the 256x128 tiles (all M rows with 256
     // weight rows) fit in one round: a CU then reads the activations once per
     // 256 weight rows instead of once per 128, and no partial second round
@@ -292,6 +365,40 @@ GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
   // 256x256 tiles (M=512, N=7168, K=18432 and M=1024: 89 / 150 us against
   // 115-132 / 189 us on 128x128 tiles)
   if (kg % 2 == 0 && (t256 >= cus || kg >= 96)) return {kPerN256M256, tail_split()};
+  if (m <= 512 && t128 < cus) {
+    // Up to 512 rows with fewer 128x128 tiles than CUs the product is still
+    // HBM-bound: the weight read decides, and the 128x128 tiles leave CUs
+    // idle.  First the wide decode tiles where they fill one round; else the
+    // 64x64 LDS-staged tiles where they fit one round (from 48 scale groups
+    // up only where they fit one per CU); else, with an even number of 48
+    // scale groups or more, the persistent 128x128 tiles with their tail
+    // split (all tiles in one, partial round, cut in up to 8 K ranges: the
+    // fp32 partial round trip pays off only over a long K, at K=4096 it
+    // loses 27.6 against 19.0 us); else the 128x128 tiles, split so that
+    // the fp32 partials of all splits (4 * split * M bytes a column) stay
+    // within half the weight bytes (M=448, N=6144, K=4096: 35.5 us in two,
+    // 26.5 unsplit).  Same box, us (before: 128x128 tiles, K split in 3):
+    // M=160, N=1536, K=7168 32.4 -> 11.1; M=192, N=4096, K=7168 35.8 ->
+    // 21.2; N=576 31.5 -> 11.2; N=2112 32.2 -> 15.8; N=7168, K=2048 15.6 ->
+    // 12.3; N=3072, K=1536 12.7 -> 8.6; M=256, N=4608, K=7168 36.9 -> 29.8;
+    // M=384, N=4096, K=7168 44.9 -> 34.4; N=1536 33.6 -> 17.4; N=4096, K=512
+    // 7.0 -> 5.9; M=160, N=6144, K=4096 27.6 (128x128, tail split) -> 19.0.
+    GemmChoice wc;
+    if (wide_tiles(&wc)) return wc;
+    const int64_t t64 = ((n + 63) / 64) * ((m + 63) / 64);
+    if (t64 <= cus || (kg < 48 && t64 <= 2 * cus)) return {kPreN64M64S4, lds64_split(t64)};
+    if (kg % 2 == 0 && kg >= 48) return {kPerN128M128, 8};
+    int64_t split = (cus + t128 - 1) / t128;
+    if (split > 4) split = 4;
+    if (split > kg / 16) split = kg / 16;
+    while (split > 1 && 8 * split * m > k) --split;
+    return {kPreN128M128S2, int32_t(split < 1 ? 1 : split)};
+  }
+  // Up to 256 rows (one 256-row tile) and 48 scale groups or more, with as
+  // many 128x128 tiles as CUs or more: the persistent 256x256 tiles with
+  // their tail split (M=160, N=18432, K=7168 65.6 -> 61.0 us; M=224 74.3 ->
+  // 63.1)
+  if (m <= 256 && kg % 2 == 0 && kg >= 48) return {kPerN256M256, tail_split()};
   // Otherwise: a 256x256 tile runs alone on a CU and does four 128x128 tiles'
   // work in about 1.5x their time (two 128x128 tiles share a CU); count whole
   // rounds of workgroups for both and take the cheaper one.

@@ -196,6 +196,43 @@ def test_config3_m_sweep_all_elements(m, nk):
     _check_full(a, aq, as_, bq, bs, outs, rows, f"config3 {m}x{n}x{k}")
 
 
+# One shape per branch of the automatic tile choice between the decode and
+# the prefill sizes (17-512 rows), each named with the configuration and K
+# split the host picks for it (checked by the host tests); every element of
+# the automatically launched product is compared.
+SELECTION_SHAPES = [
+    (24, 4096, 7168),     # 64x32 wide tiles, K in 4
+    (24, 24576, 1536),    # 64x64 LDS-staged tiles beyond two stripes per CU
+    (48, 7168, 18432),    # 128x64 LDS-staged tiles, K in 4
+    (72, 4608, 7168),     # 64x32 wide tiles unsplit
+    (96, 576, 7168),      # 64x32 wide tiles, row groups not a multiple of 8
+    (96, 24576, 1536),    # 128x128 tiles
+    (96, 18432, 7168),    # persistent 128x128 tiles, tail split
+    (160, 1536, 7168),    # 64x32 wide tiles, K in 2
+    (192, 4096, 7168),    # 64x64 wide tiles
+    (150, 1000, 7168),    # ragged N and M on wide tiles
+    (448, 2048, 10240),   # 64x64 LDS-staged tiles, K in 2 (M x K beyond L2)
+    (384, 4096, 7168),    # persistent 128x128 tiles, tail split
+    (448, 6144, 4096),    # 128x128 tiles unsplit
+    (300, 2500, 5120),    # ragged, 64x64 wide tiles
+    (300, 2600, 5120),    # ragged, 64x64 LDS-staged tiles, K in 2
+    (160, 18432, 7168),   # persistent 256x256 tiles, tail split
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m,n,k", SELECTION_SHAPES)
+def test_selected_kernels_mid_m_all_elements(m, n, k):
+    device()
+    cfg, split = inferop_amd.gemm_select(m, n, k)
+    what = f"m={m} n={n} k={k} {inferop_amd.gemm_config_name(cfg)}:{split}"
+    print(what, flush=True)
+    a, aq, as_, bq, bs = _device_case(m, n, k, seed=400 + m)
+    rows = np.unique(np.concatenate([[0, m - 1], np.random.default_rng(m * n).integers(0, m, 4)]))
+    outs = {out: _gemm(aq, as_, bq, bs, m, n, k, out=out) for out in ("bf16", "fp16")}
+    _check_full(a, aq, as_, bq, bs, outs, rows, what)
+
+
 N_CONFIGS = inferop_amd.gemm_num_configs()
 
 

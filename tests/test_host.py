@@ -190,8 +190,13 @@ def test_gemm_selection_covers_configs():
     assert sel(16, 7168, 7168) == ("dw_m16_k4_w3a3", 1)
     assert sel(16, 36864, 7168) == ("dw_m16_k8_w2a2", 1)
     assert sel(16, 7168, 18432) == ("dw_m16_k2_w8a8", 1)
+    # 17 <= M <= 32: the stripe kernel below 32 scale groups (64x64 LDS tiles
+    # beyond two stripes per CU), 64x32 wide tiles with K split from 32 up
     assert sel(32, 7168, 2048) == ("dw_m32_k4_w2a2", 1)
-    assert sel(32, 4096, 7168) == ("dw_m32_k4_w2a2", 1)
+    assert sel(24, 24576, 1536) == ("pre_n64_m64_w4_s4", 1)
+    assert sel(32, 4096, 7168) == ("dw_n64_m32_k4_w2a2", 4)
+    assert sel(24, 7168, 18432) == ("dw_n64_m32_k4_w2a2", 2)
+    assert sel(24, 36864, 7168) == ("dw_n64_m32_k4_w2a2", 1)
     # 33 <= M <= 64: a workgroup per 64 (or 32) weight rows, K split to fill
     # one round of CUs; two 32-row activation tiles only when N's 64-row
     # groups are a multiple of 8 (the tiles of a row group share an XCD)
@@ -199,6 +204,8 @@ def test_gemm_selection_covers_configs():
     assert sel(64, 4096, 7168) == ("dw_n64_m32_k4_w2a2", 2)
     assert sel(64, 2112, 7168) == ("dw_n32_m64_k4_w2a2", 3)
     assert sel(64, 36864, 7168) == ("pre_n128_m64_w8_s4", 2)
+    # a long K that one round of 64x32 tiles covers only unsplit: 128x64 tiles
+    assert sel(48, 7168, 18432) == ("pre_n128_m64_w8_s4", 4)
     assert sel(128, 7168, 2048) == ("dw_n64_m64_k4_w2a2", 1)
     assert sel(128, 4096, 512) == ("dw_n64_m32_k4_w2a2", 1)
     assert sel(128, 7168, 18432) == ("per_n128_m128_w4", 4)
@@ -210,10 +217,38 @@ def test_gemm_selection_covers_configs():
     # of 8: 64x64 wide decode tiles when they fill the CUs
     assert sel(100, 4096, 7168) == ("dw_n64_m64_k4_w2a2", 2)
     assert sel(96, 7168, 7168) == ("dw_n64_m64_k4_w2a2", 1)
-    assert sel(128, 2048, 4096) == ("dw_n64_m64_k4_w2a2", 4)
+    assert sel(128, 2048, 4096) == ("dw_n64_m32_k4_w2a2", 2)
     assert sel(128, 4096, 16384) == ("dw_n64_m64_k4_w2a2", 2)
-    assert sel(72, 4608, 7168)[0] == "pre_n64_m64_w4_s4"
+    # ... 32-row activation tiles where they fill the CUs on their own or with
+    # K split; a small weight whose row groups are not a multiple of 8 over
+    # at most six of them; 64x64 LDS-staged tiles otherwise, at most 6 splits
+    assert sel(72, 4608, 7168) == ("dw_n64_m32_k4_w2a2", 1)
+    assert sel(96, 1536, 7168) == ("dw_n64_m32_k4_w2a2", 3)
+    assert sel(96, 576, 7168) == ("dw_n64_m32_k4_w2a2", 7)
     assert sel(77, 4672, 7168)[0] == "pre_n64_m64_w4_s4"
+    assert sel(128, 2112, 7168) == ("pre_n64_m64_w4_s4", 6)
+    # beyond one round of two 64x64 tiles per CU: 128x128 tiles, or the
+    # persistent ones with their tail split over a long K
+    assert sel(96, 24576, 1536) == ("pre_n128_m128_w4_s2", 1)
+    assert sel(96, 18432, 7168) == ("per_n128_m128_w4", 8)
+    # 129 to 512 rows with fewer 128x128 tiles than CUs: wide decode tiles,
+    # 64x64 LDS-staged tiles, persistent 128x128 tiles from 48 scale groups,
+    # 128x128 tiles with the partials of a split within half the weight bytes
+    assert sel(160, 1536, 7168) == ("dw_n64_m32_k4_w2a2", 2)
+    assert sel(192, 4096, 7168) == ("dw_n64_m64_k4_w2a2", 1)
+    assert sel(160, 4096, 8192) == ("dw_n64_m64_k4_w2a2", 1)
+    assert sel(192, 576, 7168) == ("dw_n64_m32_k4_w2a2", 4)
+    assert sel(448, 2048, 10240) == ("pre_n64_m64_w4_s4", 2)  # M x K > 4 MB
+    assert sel(384, 576, 7168) == ("pre_n64_m64_w4_s4", 4)
+    assert sel(192, 7168, 2048) == ("pre_n64_m64_w4_s4", 1)
+    assert sel(160, 6144, 4096) == ("pre_n64_m64_w4_s4", 1)
+    assert sel(384, 4096, 7168) == ("per_n128_m128_w4", 8)
+    assert sel(448, 6144, 4096) == ("pre_n128_m128_w4_s2", 1)
+    assert sel(224, 8192, 4096) == ("pre_n64_m64_w4_s4", 1)
+    assert sel(320, 8192, 4096) == ("pre_n128_m128_w4_s2", 1)
+    # up to 256 rows with many 128x128 tiles and a long K: persistent 256x256
+    assert sel(160, 18432, 7168) == ("per_n256_m256_w8", 3)
+    assert sel(160, 24576, 1536) == ("pre_n128_m128_w4_s2", 1)
     # 256x256 prefill tiles run on the persistent kernel when K / 128 is even,
     # on the one-tile-per-workgroup kernel otherwise
     assert names[inferop_amd.gemm_select(4096, 7168, 16384)[0]] == "per_n256_m256_w8"
