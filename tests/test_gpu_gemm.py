@@ -249,6 +249,48 @@ def test_every_kernel_config_ragged(config, split):
         assert_gemm_close(out_to_f32(c), want, f"cfg{config} split{split} {out}")
 
 
+def _shifted(t, shift_bytes):
+    """A copy of t whose data starts shift_bytes past a 256-byte boundary
+    (returned with the buffer that holds it)."""
+    nbytes = t.numel() * t.element_size()
+    raw = torch.zeros(nbytes + 512, dtype=torch.uint8, device=t.device)
+    view = raw[shift_bytes:shift_bytes + nbytes]
+    view.copy_(t.contiguous().view(torch.uint8).reshape(-1))
+    out = view.view(t.dtype).reshape(t.shape)
+    assert out.data_ptr() % 16 == shift_bytes % 16
+    return raw, out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("config", range(N_CONFIGS))
+def test_every_config_with_4_byte_aligned_pointers(config):
+    # The reference asks only 4-byte alignment of its pointers
+    # (kernels/gemm/w8a8_block_fp8.cu:64,78); the kernels load 16 bytes per
+    # lane.  With every operand and C 4, 8 or 12 bytes past a 16-byte
+    # boundary each configuration gives the bits of the aligned call (C then
+    # takes the element-wise stores).
+    device()
+    m, n, k = 77, 300, 768
+    _, aq, as_, bq, bs = _host_case(m, n, k, seed=11, dist="stress")
+    want = oracle.gemm(aq, as_, bq, bs)
+    aq, as_, bq, bs = to_dev(aq), to_dev(as_), to_dev(bq), to_dev(bs)
+    name = inferop_amd.gemm_config_name(config)
+    for out in ("bf16", "fp32"):
+        c0 = _gemm(aq, as_, bq, bs, m, n, k, out, config, 1)
+        held, ops = [], []
+        for t, sh in ((aq, 4), (as_, 4), (bq, 8), (bs, 12)):
+            raw, v = _shifted(t, sh)
+            held.append(raw)
+            ops.append(v)
+        rawc, c1 = _shifted(torch.full((m, n), float("nan"), dtype=TORCH_OUT[out],
+                                       device="cuda:0"), 4)
+        st = inferop_amd.w8a8_block_fp8_gemm_config(c1, *ops, m, n, k, getattr(DT, out),
+                                                    config, 1)
+        assert st == 0
+        assert_gemm_close(out_to_f32(c1), want, f"{name} {out} shifted")
+        assert torch.equal(c0, c1), f"{name} {out}: shifted pointers change the result"
+
+
 def _cfg(name):
     return next(i for i in range(N_CONFIGS) if inferop_amd.gemm_config_name(i) == name)
 
