@@ -382,13 +382,16 @@ __global__ __launch_bounds__(256) void weight_block_quant_kernel(uint8_t* __rest
           _Float16, (uint16_t)((j & 1) ? (wv[i][j >> 1] >> 16) : (wv[i][j >> 1] & 0xFFFFu)));
     }
   };
-  // the codes of the thread's columns 0..3 (lo) and 4..7 (hi) of a row
+  // the codes of the thread's columns 0..3 (lo) and 4..7 (hi) of a row.  The
+  // weight is read once and its codes written once: both go non-temporal
+  // (7168x16384 fp32 110 -> 99 us, 36864x7168 bf16 142 -> 135 us, fp16 145 ->
+  // 136 us).
   auto store_codes = [&](uint8_t* dst, uint32_t lo, uint32_t hi) {
     if constexpr (DT == kFp32) {
-      *reinterpret_cast<uint32_t*>(dst) = lo;
-      *reinterpret_cast<uint32_t*>(dst + kHiCol) = hi;
+      __builtin_nontemporal_store(lo, reinterpret_cast<uint32_t*>(dst));
+      __builtin_nontemporal_store(hi, reinterpret_cast<uint32_t*>(dst + kHiCol));
     } else {
-      *reinterpret_cast<u32x2*>(dst) = u32x2{lo, hi};
+      __builtin_nontemporal_store(u32x2{lo, hi}, reinterpret_cast<u32x2*>(dst));
     }
   };
   uint32_t key = 0;
@@ -399,12 +402,12 @@ __global__ __launch_bounds__(256) void weight_block_quant_kernel(uint8_t* __rest
       const int64_t e = row * k + col;
       if constexpr (DT == kFp32) {
         const float* p = reinterpret_cast<const float*>(w) + e;
-        const u32x4 a = *reinterpret_cast<const u32x4*>(p);
-        const u32x4 b = *reinterpret_cast<const u32x4*>(p + kHiCol);
+        const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+        const u32x4 b = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p + kHiCol));
         wv[i][0] = a.x, wv[i][1] = a.y, wv[i][2] = a.z, wv[i][3] = a.w;
         wv[i][4] = b.x, wv[i][5] = b.y, wv[i][6] = b.z, wv[i][7] = b.w;
       } else {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(w) + e);
+        const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(w) + e));
         wv[i][0] = a.x, wv[i][1] = a.y, wv[i][2] = a.z, wv[i][3] = a.w;
       }
     } else {
