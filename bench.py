@@ -576,18 +576,21 @@ def main():
         fres = []
         # SiLU(gate) * up -> E4M3: DeepSeek-V3 MLP, 4096 tokens x d 18432, bf16
         tok, dd = 4096, 18432
+        # inputs rotated over more than 1 GiB, so the 256 MB Infinity Cache
+        # cannot serve them
+        nsilu = max(2, -(-(1 << 30) // (tok * 2 * dd * 2)))
         gus = [torch.randn((tok, 2 * dd), generator=gen, device=dev).to(torch.bfloat16)
-               for _ in range(2)]
+               for _ in range(nsilu)]
         fq = torch.empty((tok, dd), dtype=torch.uint8, device=dev)
         fs = torch.empty((tok, dd // 128), dtype=torch.float32, device=dev)
 
         def fsilu(i):
-            st = ia.silu_and_mul_quant_fp8(fq, fs, gus[i % 2], DT.bf16, tok, dd, 128, sp)
+            st = ia.silu_and_mul_quant_fp8(fq, fs, gus[i % nsilu], DT.bf16, tok, dd, 128, sp)
             assert st == 0, st
 
-        gf = capture(lambda: [fsilu(i) for i in range(4)])
+        gf = capture(lambda: [fsilu(i) for i in range(nsilu)])
         time_graphs([gf], 2)
-        us = time_graphs([gf], 5) / 4 * 1e3
+        us = time_graphs([gf], 5) / nsilu * 1e3
         fb = tok * dd * (2 * 2 + 1) + 4 * tok * (dd // 128)
         fres.append({"op": "silu_and_mul_quant_fp8", "tokens": tok, "d": dd, "dtype": "bfloat16",
                      "us": round(us, 2), "gbs": round(fb / (us * 1e-6) / 1e9, 1),
@@ -595,21 +598,24 @@ def main():
         del gus, fq, fs, gf
         # residual += x; RMSNorm -> E4M3: 4096 rows x 7168 (the hidden size), bf16
         rows, cols = 4096, 7168
-        res_ = torch.randn((rows, cols), generator=gen, device=dev).to(torch.bfloat16)
+        # (residual, x) pairs rotated over more than 1 GiB
+        nrms = max(2, -(-(1 << 30) // (rows * cols * 2 * 2)))
+        res_ = [torch.randn((rows, cols), generator=gen, device=dev).to(torch.bfloat16)
+                for _ in range(nrms)]
         xs_ = [torch.randn((rows, cols), generator=gen, device=dev).to(torch.bfloat16) * 0.01
-               for _ in range(2)]
+               for _ in range(nrms)]
         wn = torch.ones((cols,), dtype=torch.bfloat16, device=dev)
         fq = torch.empty((rows, cols), dtype=torch.uint8, device=dev)
         fs = torch.empty((rows, cols // 128), dtype=torch.float32, device=dev)
 
         def frms(i):
-            st = ia.fused_add_rmsnorm_quant_fp8(res_, fq, fs, xs_[i % 2], wn, DT.bf16, rows, cols,
-                                                1e-6, 128, sp)
+            st = ia.fused_add_rmsnorm_quant_fp8(res_[i % nrms], fq, fs, xs_[i % nrms], wn, DT.bf16,
+                                                rows, cols, 1e-6, 128, sp)
             assert st == 0, st
 
-        gf = capture(lambda: [frms(i) for i in range(4)])
+        gf = capture(lambda: [frms(i) for i in range(nrms)])
         time_graphs([gf], 2)
-        us = time_graphs([gf], 5) / 4 * 1e3
+        us = time_graphs([gf], 5) / nrms * 1e3
         fb = rows * cols * (3 * 2 + 1) + 2 * cols + 4 * rows * (cols // 128)
         fres.append({"op": "fused_add_rmsnorm_quant_fp8", "rows": rows, "cols": cols,
                      "dtype": "bfloat16", "us": round(us, 2),
