@@ -546,6 +546,31 @@ def main():
             qres.append({"m": mq, "k": kq, "us": round(us, 2), "gbs": round(gbs, 1),
                          "frac": round(gbs / HBM_PEAK_GBS, 4)})
             del xs, q, s, gq
+        # ---------------- dequantizer (E4M3 + group scales -> dt) ----------------
+        dres = []
+        for (md, kd, odt) in ((4096, 7168, torch.bfloat16), (8192, 18432, torch.bfloat16),
+                              (4096, 7168, torch.float32)):
+            ob = 4 if odt == torch.float32 else 2
+            nbuf = max(2, -(-(1 << 30) // (md * kd * (1 + ob))))
+            dq = [rand_fp8((md, kd)) for _ in range(nbuf)]
+            ds_ = [rand_scales((md, kd // 128)) for _ in range(nbuf)]
+            dx = [torch.empty((md, kd), dtype=odt, device=dev) for _ in range(nbuf)]
+            dcode = DT.fp32 if odt == torch.float32 else DT.bf16
+
+            def fdq(i, md=md, kd=kd, dq=dq, ds_=ds_, dx=dx, dcode=dcode, nbuf=nbuf):
+                st = ia.dequant_fp8_per_token_group(dx[i % nbuf], dcode, dq[i % nbuf],
+                                                    ds_[i % nbuf], md, kd, 128, sp)
+                assert st == 0, st
+
+            gd = capture(lambda: [fdq(i) for i in range(nbuf)])
+            time_graphs([gd], 2)
+            us = time_graphs([gd], 5) / nbuf * 1e3
+            db = md * kd * (1 + ob) + 4 * md * (kd // 128)
+            dres.append({"m": md, "k": kd, "dtype": str(odt).replace("torch.", ""),
+                         "us": round(us, 2), "gbs": round(db / (us * 1e-6) / 1e9, 1),
+                         "frac": round(db / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+            del dq, ds_, dx, gd
+        result["dequant"] = {"shapes": dres, "peak_gbs": HBM_PEAK_GBS}
         # ---------------- weight block quantizer (weight-load time) ----------------
         wres = []
         for (nw, kw, wdt) in ((7168, 16384, torch.float32), (36864, 7168, torch.bfloat16)):

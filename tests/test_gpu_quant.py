@@ -135,7 +135,7 @@ def test_quant_large_sampled_rows_and_roundtrip():
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("out", ["fp32", "bf16", "fp16"])
-@pytest.mark.parametrize("gs", [128, 64, 48, 40])
+@pytest.mark.parametrize("gs", [128, 64, 48, 40, 36])  # 36: the element-wise path
 def test_dequant_parity(out, gs):
     device()
     m, k = 37, gs * 8
@@ -185,7 +185,7 @@ def _fp16_tie_cases():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("gs", [128, 64, 48, 40])
+@pytest.mark.parametrize("gs", [128, 64, 48, 40, 36])
 def test_dequant_fp16_rounds_through_fp32(gs):
     """fp16 output is the fp32 product rounded to fp16 (two roundings, as in
     the reference), not the exact product rounded once: every group here is
