@@ -70,7 +70,9 @@ def test_silu_quant_every_gate_value(kind):
     vals = vals[np.isfinite(vals)]
     d = 1024
     n = (len(vals) // d) * d
-    gate = vals[:n].reshape(-1, d)
+    # repeated 17 times in shifted order: 8568 groups, enough for the bf16
+    # kernel that copies its SiLU table slice into LDS (a full step per CU)
+    gate = np.concatenate([np.roll(vals[:n], 97 * r) for r in range(17)]).reshape(-1, d)
     tokens = gate.shape[0]
     g = np.random.default_rng(31)
     for up in (np.ones_like(gate), g.standard_normal(gate.shape).astype(np.float32)):
@@ -83,8 +85,31 @@ def test_silu_quant_every_gate_value(kind):
         assert bad_q <= q.size // 10000 and bad_s <= s.size // 1000, (bad_q, bad_s)
 
 
+def test_silu_bf16_lds_table_matches_global_table():
+    # 8200 tokens x 128 outputs = 8200 groups take the kernel that holds the
+    # SiLU table slice in LDS; 64-token calls (64 groups) take the kernel
+    # that gathers from the full table.  Rows are independent, so both must
+    # give the same bits for every bf16 gate pattern, Inf and NaN included.
+    device()
+    tokens, d = 8200, 128
+    pats = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    reps = -(-tokens * d // 65536)
+    gate = np.concatenate([np.roll(pats, 131 * r) for r in range(reps)])[: tokens * d]
+    g = np.random.default_rng(8200)
+    up = f32_to_bf16_bits((2.0 * g.standard_normal(tokens * d)).astype(np.float32))
+    gu = np.concatenate([gate.reshape(tokens, d), up.reshape(tokens, d)], axis=1)
+    gu_dev = bf16_dev(np.ascontiguousarray(gu))
+    q, s = _silu_gpu(gu_dev, "bf16", tokens, d)
+    for r0 in range(0, tokens, 64):
+        r1 = min(tokens, r0 + 64)
+        qs, ss = _silu_gpu(gu_dev[r0:r1].contiguous(), "bf16", r1 - r0, d)
+        assert np.array_equal(qs, q[r0:r1]), r0
+        assert np.array_equal(ss.view(np.uint32), s[r0:r1].view(np.uint32)), r0
+
+
 @pytest.mark.parametrize("kind", ["bf16", "fp16", "fp32"])
-@pytest.mark.parametrize("shape", [(1, 2048), (64, 18432 // 8), (77, 7168 // 4)])
+@pytest.mark.parametrize("shape", [(1, 2048), (64, 18432 // 8), (77, 7168 // 4), (8195, 128),
+                                   (4096, 18432 // 8)])
 def test_silu_quant_parity(kind, shape):
     device()
     tokens, d = shape

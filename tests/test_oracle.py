@@ -449,3 +449,28 @@ def test_dequant_closed_form(gs):
         nan = np.isnan(want)
         assert np.array_equal(np.isnan(got), nan)
         assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_silu_bf16_exponent_rules():
+    # The bf16 SiLU kernel keeps only gates with exponent field in [102, 134)
+    # in its LDS table and computes the rest as g * 0.5 (E < 102), g (E >= 134,
+    # g > 0; also +Inf and positive NaN) or -0 (E >= 134 finite, g < 0); -Inf
+    # and negative NaN read the full table.  Check every bf16 pattern against
+    # the oracle's SiLU (reference.cpp:55-64 with up = 1).
+    bits = np.arange(65536, dtype=np.uint32)
+    gate = (bits << 16).view(np.float32)
+    gu = np.concatenate([gate.reshape(-1, 128), np.ones((512, 128), np.float32)], axis=1)
+    with np.errstate(all="ignore"):
+        want = oracle.silu_and_mul(gu).reshape(-1)
+        e = (bits >> 7) & 0xFF
+        neg = (bits >> 15) == 1
+        rule = np.where(e < 102, gate * np.float32(0.5),
+                        np.where(neg, np.float32(-0.0), gate)).astype(np.float32)
+    outside = (e < 102) | ((e >= 134) & ~(neg & (e == 255)))
+    got, exp = rule[outside], want[outside]
+    same = (got.view(np.uint32) == exp.view(np.uint32)) | (np.isnan(got) & np.isnan(exp))
+    assert same.all(), bits[outside][~same][:8]
+    assert (np.signbit(got) == np.signbit(exp)).all()
+    # the rules are not vacuous: inside the table range they fail somewhere
+    inside = (e >= 102) & (e < 134)
+    assert (rule[inside].view(np.uint32) != want[inside].view(np.uint32)).sum() > 1000
