@@ -784,11 +784,12 @@ __global__ __launch_bounds__(256) void add_rmsnorm_quant_kernel(
   const uint8_t* xr = reinterpret_cast<const uint8_t*>(x) + row * cols * EB;
   // pass 1 stores residual = dt(residual + x) and sums the squares of the
   // stored values; the first kKeep column blocks (cols <= 8192) keep those
-  // values in registers for pass 2, longer rows read the rest back
+  // values in registers for pass 2 (as the stored dt words: half the
+  // registers for 16-bit types), longer rows read the rest back
   constexpr int kKeep = 4;
-  float keep[kKeep][8];
+  uint32_t keep[kKeep][In<DT>::kWords];
   float ss = 0.0f;
-  auto pass1 = [&](int64_t c, float* stored) {
+  auto pass1 = [&](int64_t c, uint32_t* kept) {
     float rv[8], xv[8];
     load_dt8<DT>(res + c * EB, rv);
     load_dt8<DT>(xr + c * EB, xv);
@@ -802,19 +803,21 @@ __global__ __launch_bounds__(256) void add_rmsnorm_quant_kernel(
     } else {
       *reinterpret_cast<u32x4*>(res + c * EB) = u32x4{w[0], w[1], w[2], w[3]};
     }
+    float stored[8];
     load_dt8<DT>(w, stored);
 #pragma unroll
     for (int i = 0; i < 8; ++i) ss += stored[i] * stored[i];
+    if (kept) {
+#pragma unroll
+      for (int i = 0; i < In<DT>::kWords; ++i) kept[i] = w[i];
+    }
   };
 #pragma unroll
   for (int it = 0; it < kKeep; ++it) {
     const int64_t c = (int64_t)t * 8 + it * 2048;
     if (c < cols) pass1(c, keep[it]);
   }
-  for (int64_t c = (int64_t)t * 8 + kKeep * 2048; c < cols; c += 2048) {
-    float stored[8];
-    pass1(c, stored);
-  }
+  for (int64_t c = (int64_t)t * 8 + kKeep * 2048; c < cols; c += 2048) pass1(c, nullptr);
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
   if ((t & 63) == 0) red[t >> 6] = ss;
@@ -825,15 +828,14 @@ __global__ __launch_bounds__(256) void add_rmsnorm_quant_kernel(
   const uint8_t* wt = reinterpret_cast<const uint8_t*>(weight);
   // pass 2: out = dt((residual * inv) * weight), quantized per 128 columns;
   // kept values come from registers, the rest from this thread's own stores
-  auto pass2 = [&](int64_t c0, const float* kept) {
+  auto pass2 = [&](int64_t c0, const uint32_t* kept) {
     const int64_t c = c0 + (int64_t)t * 8;
     const bool live = c < cols;  // whole 16-lane groups, since cols % 128 == 0
     float y[8];
     if (live) {
       float rv[8], wv[8];
       if (kept) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) rv[i] = kept[i];
+        load_dt8<DT>(kept, rv);
       } else {
         load_dt8<DT>(res + c * EB, rv);
       }
