@@ -600,9 +600,34 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return silu_of(g) 
 // evaluates the arithmetic instead, and both give the same bits.
 __device__ float silu_table_bf16[65536];
 
+// For fp16 gates exp(-g) = exp(-g_hi) * exp(-g_lo) in double, where g_hi
+// is g with its low 7 mantissa bits cleared and g_lo = g - g_hi (exact):
+// 512 + 8192 doubles indexed by (sign, exponent field, top 3 / low 7 mantissa
+// bits), filled with the device's double exponential.  The product carries
+// the same few double ulps of error as one exp call, so rounding it to fp32
+// gives the value silu_of uses except within ~2^-50 relative of an fp32
+// rounding midpoint.
+__device__ double silu_exp_hi_f16[512];
+__device__ double silu_exp_lo_f16[8192];
+
+// fp16 value of (sign, exponent field, mantissa) in double (exact).
+__device__ __forceinline__ double f16_parts(uint32_t s, uint32_t e, uint32_t m) {
+  const double mag = e == 0 ? ldexp((double)m, -24) : ldexp((double)(1024 + m), (int)e - 25);
+  return s ? -mag : mag;
+}
+
 __global__ __launch_bounds__(256) void silu_table_build_kernel() {
   const uint32_t b = blockIdx.x * 256 + threadIdx.x;
   silu_table_bf16[b] = silu_of(u2f(b << 16));
+  if (b < 8192) {  // (sign, exponent, low 7 bits): exp(-g_lo)
+    const uint32_t s = b >> 12, e = (b >> 7) & 31, ml = b & 127;
+    const double gl = f16_parts(s, e, ml) - f16_parts(s, e, 0);
+    silu_exp_lo_f16[b] = ::exp(-gl);
+  }
+  if (b < 512) {  // (sign, exponent, top 3 bits): exp(-g_hi)
+    const uint32_t s = b >> 8, e = (b >> 3) & 31, mh = b & 7;
+    silu_exp_hi_f16[b] = ::exp(-f16_parts(s, e, mh << 7));
+  }
 }
 
 // Most of the table is one of three exact rules.  For a bf16 gate g with
@@ -644,19 +669,40 @@ __device__ __forceinline__ float silu_bf16_lds(const float* tab, uint32_t gbits)
   return rel < 32u ? t : rule;
 }
 
-// gate_up: [tokens, 2d] bf16 -> q [tokens, d] E4M3, scales [tokens, d/128],
-// with the table slice in LDS.  Lane layout as silu_mul_quant_kernel (16
+// fp16 gate g (exactly representable) -> silu(g) from the two LDS tables
+// (tlo: 8192 doubles, thi: 512); Inf / NaN gates are left to the caller.
+__device__ __forceinline__ float silu_f16_lds(const double* tlo, const double* thi, float g) {
+  const uint32_t b = __builtin_bit_cast(uint16_t, (_Float16)g);
+  const double p = thi[b >> 7] * tlo[((b & 0xFC00u) >> 3) | (b & 127u)];
+  return g / (1.0f + (float)p);
+}
+
+// gate_up: [tokens, 2d] dt (bf16 or fp16) -> q [tokens, d] E4M3, scales
+// [tokens, d/128], with the tables in LDS (bf16: the 32 KB SiLU slice; fp16:
+// the 68 KB exponential pair).  Lane layout as silu_mul_quant_kernel (16
 // lanes per 128-output group, 4 groups per wave and step, U steps issued
 // together); NT-thread workgroups stride over the groups so each copies the
-// slice once, and large workgroups let more waves share one copy.
-template <int U, int NT>
+// tables once, and large workgroups let more waves share one copy.
+template <int DT, int U, int NT>
 __global__ __launch_bounds__(NT) void silu_mul_quant_lds_kernel(uint8_t* __restrict__ q,
                                                                  float* __restrict__ scales,
                                                                  const uint16_t* __restrict__ gate_up,
                                                                  uint32_t d, uint32_t gpr,
                                                                  uint32_t ngroups) {
-  __shared__ __align__(16) float tab[kSiluLdsEntries];
-  silu_lds_fill<NT>(tab);
+  static_assert(DT == kBf16 || DT == kFp16, "16-bit gates only");
+  constexpr int kBytes = DT == kBf16 ? kSiluLdsEntries * 4 : (8192 + 512) * 8;
+  __shared__ __align__(16) uint8_t lds[kBytes];
+  float* tab = reinterpret_cast<float*>(lds);
+  double* tlo = reinterpret_cast<double*>(lds);
+  double* thi = tlo + 8192;
+  if constexpr (DT == kBf16) {
+    silu_lds_fill<NT>(tab);
+  } else {
+    const u32x4* lo = reinterpret_cast<const u32x4*>(silu_exp_lo_f16);
+    const u32x4* hi = reinterpret_cast<const u32x4*>(silu_exp_hi_f16);
+    u32x4* dst = reinterpret_cast<u32x4*>(lds);
+    for (int v = threadIdx.x; v < 4096 + 256; v += NT) dst[v] = v < 4096 ? lo[v] : hi[v - 4096];
+  }
   __syncthreads();
   const int lane = threadIdx.x & 63;
   const int sub = lane & 15;
@@ -673,8 +719,8 @@ __global__ __launch_bounds__(NT) void silu_mul_quant_lds_kernel(uint8_t* __restr
       gc[u] = g - t[u] * gpr;
       if (g < ngroups) {
         const uint16_t* row = gate_up + (uint64_t)t[u] * 2 * d + gc[u] * 128 + sub * 8;
-        load_dt8<kBf16, true>(row, gv[u]);
-        load_dt8<kBf16, true>(row + d, uv[u]);
+        load_dt8<DT, true>(row, gv[u]);
+        load_dt8<DT, true>(row + d, uv[u]);
       } else {
 #pragma unroll
         for (int i = 0; i < 8; ++i) gv[u][i] = uv[u][i] = 0.0f;
@@ -684,24 +730,37 @@ __global__ __launch_bounds__(NT) void silu_mul_quant_lds_kernel(uint8_t* __restr
     for (int u = 0; u < U; ++u) {
       const uint32_t g = (uint32_t)base + 4 * u + (lane >> 4);
       float y[8];
-      bool neg_special = false;
+      bool special = false;
+      if constexpr (DT == kBf16) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        y[i] = silu_bf16_lds(tab, f2u(gv[u][i]));
-        neg_special |= (f2u(gv[u][i]) >> 23) == 0x1FFu;
-      }
-      if (neg_special) {
+        for (int i = 0; i < 8; ++i) {
+          y[i] = silu_bf16_lds(tab, f2u(gv[u][i]));
+          special |= (f2u(gv[u][i]) >> 23) == 0x1FFu;
+        }
+        if (special) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-          if ((f2u(gv[u][i]) >> 23) == 0x1FFu) y[i] = silu_table_bf16[f2u(gv[u][i]) >> 16];
+          for (int i = 0; i < 8; ++i)
+            if ((f2u(gv[u][i]) >> 23) == 0x1FFu) y[i] = silu_table_bf16[f2u(gv[u][i]) >> 16];
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          y[i] = silu_f16_lds(tlo, thi, gv[u][i]);
+          special |= (f2u(gv[u][i]) & 0x7F800000u) == 0x7F800000u;
+        }
+        if (special) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            if ((f2u(gv[u][i]) & 0x7F800000u) == 0x7F800000u) y[i] = silu_of(gv[u][i]);
+        }
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i) y[i] *= uv[u][i];
-      uint32_t w[In<kBf16>::kWords];
-      pack_dt8<kBf16>(y, w);
+      uint32_t w[In<DT>::kWords];
+      pack_dt8<DT>(y, w);
       uint32_t lo, hi;
       float s;
-      quant_group_lane<kBf16>(w, lo, hi, s);
+      quant_group_lane<DT>(w, lo, hi, s);
       if (g < ngroups) {
         __builtin_nontemporal_store(
             u32x2{lo, hi},
@@ -928,6 +987,23 @@ hipError_t launch_silu_mul_quant(uint8_t* q, float* scales, const void* gate_up,
                                  int64_t d, hipStream_t st) {
   const int use_table = DT == kBf16 && silu_table(st) ? 1 : 0;
   const int64_t ngroups = tokens * (d / 128);
+  if constexpr (DT == kFp16) {
+    if (silu_table(st)) {
+      // 68 KB of LDS per workgroup: two 512-thread workgroups per CU
+      constexpr int UL = 2, NT = 512, kWgPerCu = 2;
+      constexpr int kStep = NT / 16 * UL;
+      int cus = 0;
+      if (hipError_t e = silu_device_cus(&cus); e != hipSuccess) return e;
+      if (ngroups >= (int64_t)kStep * cus && ngroups <= 0xFFFFFFFFll) {
+        const int64_t steps = (ngroups + kStep - 1) / kStep;
+        const int64_t blocks = steps < (int64_t)cus * kWgPerCu ? steps : (int64_t)cus * kWgPerCu;
+        hipLaunchKernelGGL((silu_mul_quant_lds_kernel<kFp16, UL, NT>), dim3((unsigned)blocks),
+                           dim3(NT), 0, st, q, scales, static_cast<const uint16_t*>(gate_up),
+                           (uint32_t)d, (uint32_t)(d / 128), (uint32_t)ngroups);
+        return hipGetLastError();
+      }
+    }
+  }
   if (DT == kBf16 && use_table) {
     // the LDS slice pays for its 32 KB copy once every CU has a full step
     constexpr int UL = 2, NT = 512;
@@ -938,7 +1014,7 @@ hipError_t launch_silu_mul_quant(uint8_t* q, float* scales, const void* gate_up,
       const int64_t steps = (ngroups + kStep - 1) / kStep;
       const int64_t blocks = steps < (int64_t)cus * kSiluLdsWgPerCu ? steps
                                                                      : (int64_t)cus * kSiluLdsWgPerCu;
-      hipLaunchKernelGGL((silu_mul_quant_lds_kernel<UL, NT>), dim3((unsigned)blocks), dim3(NT), 0, st,
+      hipLaunchKernelGGL((silu_mul_quant_lds_kernel<kBf16, UL, NT>), dim3((unsigned)blocks), dim3(NT), 0, st,
                          q, scales, static_cast<const uint16_t*>(gate_up), (uint32_t)d,
                          (uint32_t)(d / 128), (uint32_t)ngroups);
       return hipGetLastError();

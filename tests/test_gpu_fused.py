@@ -70,9 +70,10 @@ def test_silu_quant_every_gate_value(kind):
     vals = vals[np.isfinite(vals)]
     d = 1024
     n = (len(vals) // d) * d
-    # repeated 17 times in shifted order: 8568 groups, enough for the bf16
-    # kernel that copies its SiLU table slice into LDS (a full step per CU)
-    gate = np.concatenate([np.roll(vals[:n], 97 * r) for r in range(17)]).reshape(-1, d)
+    # repeated 40 times in shifted order: 19840 (fp16) / 20160 (bf16)
+    # groups, enough for the kernel that copies its SiLU tables into LDS (64
+    # groups per CU: 16384 on 256 CUs)
+    gate = np.concatenate([np.roll(vals[:n], 97 * r) for r in range(40)]).reshape(-1, d)
     tokens = gate.shape[0]
     g = np.random.default_rng(31)
     for up in (np.ones_like(gate), g.standard_normal(gate.shape).astype(np.float32)):
@@ -85,30 +86,35 @@ def test_silu_quant_every_gate_value(kind):
         assert bad_q <= q.size // 10000 and bad_s <= s.size // 1000, (bad_q, bad_s)
 
 
-def test_silu_bf16_lds_table_matches_global_table():
-    # 8200 tokens x 128 outputs = 8200 groups take the kernel that holds the
-    # SiLU table slice in LDS; 64-token calls (64 groups) take the kernel
-    # that gathers from the full table.  Rows are independent, so both must
-    # give the same bits for every bf16 gate pattern, Inf and NaN included.
+@pytest.mark.parametrize("kind", ["bf16", "fp16"])
+def test_silu_lds_tables_match_small_call_kernel(kind):
+    # 32768 tokens x 128 outputs = 32768 groups take the kernel that holds
+    # its SiLU tables in LDS (it needs 64 groups per CU: 16384 on 256 CUs);
+    # 512-token calls take the kernel that gathers from the full bf16 table
+    # or evaluates the double exponential for fp16.  Rows are independent, so
+    # both must give the same bits for every 16-bit gate pattern, Inf and NaN
+    # included (fp16: exp(-g_hi) * exp(-g_lo) in double rounds to the same
+    # fp32 as one exp call for every pattern).
     device()
-    tokens, d = 8200, 128
+    tokens, d = 32768, 128
     pats = np.arange(65536, dtype=np.uint32).astype(np.uint16)
     reps = -(-tokens * d // 65536)
     gate = np.concatenate([np.roll(pats, 131 * r) for r in range(reps)])[: tokens * d]
     g = np.random.default_rng(8200)
-    up = f32_to_bf16_bits((2.0 * g.standard_normal(tokens * d)).astype(np.float32))
-    gu = np.concatenate([gate.reshape(tokens, d), up.reshape(tokens, d)], axis=1)
-    gu_dev = bf16_dev(np.ascontiguousarray(gu))
-    q, s = _silu_gpu(gu_dev, "bf16", tokens, d)
-    for r0 in range(0, tokens, 64):
-        r1 = min(tokens, r0 + 64)
-        qs, ss = _silu_gpu(gu_dev[r0:r1].contiguous(), "bf16", r1 - r0, d)
+    up32 = (2.0 * g.standard_normal(tokens * d)).astype(np.float32)
+    up = f32_to_bf16_bits(up32) if kind == "bf16" else up32.astype(np.float16).view(np.uint16)
+    gu = np.ascontiguousarray(np.concatenate([gate.reshape(tokens, d), up.reshape(tokens, d)], axis=1))
+    gu_dev = bf16_dev(gu) if kind == "bf16" else f16_dev(gu)
+    q, s = _silu_gpu(gu_dev, kind, tokens, d)
+    for r0 in range(0, tokens, 512):
+        r1 = min(tokens, r0 + 512)
+        qs, ss = _silu_gpu(gu_dev[r0:r1].contiguous(), kind, r1 - r0, d)
         assert np.array_equal(qs, q[r0:r1]), r0
         assert np.array_equal(ss.view(np.uint32), s[r0:r1].view(np.uint32)), r0
 
 
 @pytest.mark.parametrize("kind", ["bf16", "fp16", "fp32"])
-@pytest.mark.parametrize("shape", [(1, 2048), (64, 18432 // 8), (77, 7168 // 4), (8195, 128),
+@pytest.mark.parametrize("shape", [(1, 2048), (64, 18432 // 8), (77, 7168 // 4), (16411, 128),
                                    (4096, 18432 // 8)])
 def test_silu_quant_parity(kind, shape):
     device()
