@@ -593,11 +593,12 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return silu_of(g) 
 // multiply per element (4096x18432: 146 -> 111 us on one box).  The gates of
 // a layer touch a few thousand entries, which stay in the L1 cache.  fp16
 // gates, with 10-bit mantissas, spread over about 8 times as many entries and
-// the gathers then cost more than the arithmetic (181 us against about 146 us),
-// so they are computed.  One table per GPU (static device memory, held until
-// the process ends), built by silu_table_build_kernel at the first bf16 call
-// on the device (see launch_silu_mul_quant); a launch that finds no table
-// evaluates the arithmetic instead, and both give the same bits.
+// gathers from a full fp16 table cost more than the arithmetic (181 us against
+// about 146 us); small fp16 calls compute, large ones use the exponential
+// pair below from LDS.  One set of tables per GPU (static device memory, held
+// until the process ends), built by silu_table_build_kernel at the first bf16
+// or fp16 call on the device (see launch_silu_mul_quant); a launch that finds
+// no table evaluates the arithmetic instead, and both give the same bits.
 __device__ float silu_table_bf16[65536];
 
 // For fp16 gates exp(-g) = exp(-g_hi) * exp(-g_lo) in double, where g_hi
