@@ -599,28 +599,32 @@ def main():
 
         # ---------------- producers fused with the quantizer ----------------
         fres = []
-        # SiLU(gate) * up -> E4M3: DeepSeek-V3 MLP, 4096 tokens x d 18432, bf16
+        # SiLU(gate) * up -> E4M3: DeepSeek-V3 MLP, 4096 tokens x d 18432,
+        # bf16 and fp16 gates
         tok, dd = 4096, 18432
         # inputs rotated over more than 1 GiB, so the 256 MB Infinity Cache
         # cannot serve them
         nsilu = max(2, -(-(1 << 30) // (tok * 2 * dd * 2)))
-        gus = [torch.randn((tok, 2 * dd), generator=gen, device=dev).to(torch.bfloat16)
-               for _ in range(nsilu)]
         fq = torch.empty((tok, dd), dtype=torch.uint8, device=dev)
         fs = torch.empty((tok, dd // 128), dtype=torch.float32, device=dev)
+        for tdt, sdt, dname in ((torch.bfloat16, DT.bf16, "bfloat16"),
+                                (torch.float16, DT.fp16, "float16")):
+            gus = [torch.randn((tok, 2 * dd), generator=gen, device=dev).to(tdt)
+                   for _ in range(nsilu)]
 
-        def fsilu(i):
-            st = ia.silu_and_mul_quant_fp8(fq, fs, gus[i % nsilu], DT.bf16, tok, dd, 128, sp)
-            assert st == 0, st
+            def fsilu(i):
+                st = ia.silu_and_mul_quant_fp8(fq, fs, gus[i % nsilu], sdt, tok, dd, 128, sp)
+                assert st == 0, st
 
-        gf = capture(lambda: [fsilu(i) for i in range(nsilu)])
-        time_graphs([gf], 2)
-        us = time_graphs([gf], 5) / nsilu * 1e3
-        fb = tok * dd * (2 * 2 + 1) + 4 * tok * (dd // 128)
-        fres.append({"op": "silu_and_mul_quant_fp8", "tokens": tok, "d": dd, "dtype": "bfloat16",
-                     "us": round(us, 2), "gbs": round(fb / (us * 1e-6) / 1e9, 1),
-                     "frac": round(fb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
-        del gus, fq, fs, gf
+            gf = capture(lambda: [fsilu(i) for i in range(nsilu)])
+            time_graphs([gf], 2)
+            us = time_graphs([gf], 5) / nsilu * 1e3
+            fb = tok * dd * (2 * 2 + 1) + 4 * tok * (dd // 128)
+            fres.append({"op": "silu_and_mul_quant_fp8", "tokens": tok, "d": dd, "dtype": dname,
+                         "us": round(us, 2), "gbs": round(fb / (us * 1e-6) / 1e9, 1),
+                         "frac": round(fb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+            del gus, gf
+        del fq, fs
         # residual += x; RMSNorm -> E4M3: 4096 rows x 7168 (the hidden size), bf16
         rows, cols = 4096, 7168
         # (residual, x) pairs rotated over more than 1 GiB
