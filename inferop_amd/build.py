@@ -35,10 +35,18 @@ HIP_FLAGS = [
 # destination registers
 EXTRA_FLAGS = {"gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
                "device.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# sources whose per-kernel resource usage (registers, scratch, occupancy) the
+# compiler reports into _build/<source>.resources.txt rather than the console;
+# tests/test_kernel_resources.py reads it
+RESOURCE_REPORT = ("gemm.hip", "quant.hip")
+RESOURCE_FLAG = "-Rpass-analysis=kernel-resource-usage"
 CXX_FLAGS = ["-O2", "-fPIC", "-std=c++17", "-I" + INCLUDE, "-I" + CSRC, "-Wall", "-Wextra"]
 
 
-def _run(cmds, verbose):
+def _run(cmds, verbose, reports=None):
+    """Run the commands in parallel; reports maps a command's index to a file
+    that receives its compiler output instead of the console."""
+    reports = reports or {}
     procs = []
     for cmd in cmds:
         if verbose:
@@ -46,10 +54,15 @@ def _run(cmds, verbose):
         procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
                                             text=True)))
     failed = []
-    for cmd, p in procs:
+    for i, (cmd, p) in enumerate(procs):
         out, _ = p.communicate()
         out = "\n".join(l for l in out.splitlines()
                         if "packed-fp32-ops' is not a recognized feature" not in l)
+        if i in reports:
+            with open(reports[i], "w") as f:
+                f.write(out + "\n")
+            if p.returncode == 0:
+                continue
         if p.returncode != 0:
             failed.append((cmd, out))
         elif verbose and out.strip():
@@ -63,17 +76,20 @@ def _run(cmds, verbose):
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     t0 = time.time()
-    objs, cmds = [], []
+    objs, cmds, reports = [], [], {}
     for src in HIP_SOURCES:
         obj = os.path.join(BUILD, src + ".o")
         objs.append(obj)
-        cmds.append([HIPCC, *HIP_FLAGS, *EXTRA_FLAGS.get(src, []), "-c", os.path.join(CSRC, src),
-                     "-o", obj])
+        extra = list(EXTRA_FLAGS.get(src, []))
+        if src in RESOURCE_REPORT:
+            extra.append(RESOURCE_FLAG)
+            reports[len(cmds)] = os.path.join(BUILD, src + ".resources.txt")
+        cmds.append([HIPCC, *HIP_FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj])
     for src in CXX_SOURCES:
         obj = os.path.join(BUILD, src + ".o")
         objs.append(obj)
         cmds.append([CXX, *CXX_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
-    _run(cmds, verbose)
+    _run(cmds, verbose, reports)
     tmp = LIB + ".tmp"
     _run([[HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs]], verbose)
     os.replace(tmp, LIB)

@@ -247,7 +247,11 @@ __device__ __forceinline__ bool splitk_fixup(const GemmArgs& a, f32x4 (&part)[LP
     // The partials of ZB splits for QB pairs are loaded together before any
     // is added, so the loads travel in parallel rather than one split at a
     // time; each element still adds the splits in order 0, 1, ..., split - 1.
-    // No load is issued past the last split.
+    // No load is issued past the last split.  The batch loops run their full
+    // constant trip count with the split bound as a predicate (split is
+    // uniform: a scalar branch), not as a `break`: a loop with an exit cannot
+    // be unrolled, and the batch v[][] indexed by a loop variable would then
+    // live in scratch memory rather than registers.
     constexpr int QB = LP < 4 ? LP : 4;
     constexpr int ZB = (LP <= 2 ? 16 : 8) / QB;
     static_assert(LP % QB == 0, "pairs in whole batches");
@@ -260,17 +264,17 @@ __device__ __forceinline__ bool splitk_fixup(const GemmArgs& a, f32x4 (&part)[LP
         f32x4 v[ZB][QB];
 #pragma unroll
         for (int zb = 0; zb < ZB; ++zb) {
-          if (z0 + zb >= split) break;  // split is uniform: no divergence
+          const bool live = z0 + zb < split;
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb)
-            if (valid(q0 + qb)) v[zb][qb] = load(z0 + zb, q0 + qb);
+            if (live && valid(q0 + qb)) v[zb][qb] = load(z0 + zb, q0 + qb);
         }
 #pragma unroll
         for (int zb = 0; zb < ZB; ++zb) {
-          if (z0 + zb >= split) break;
+          const bool live = z0 + zb < split;
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb)
-            if (valid(q0 + qb)) sum[qb] += v[zb][qb];
+            if (live && valid(q0 + qb)) sum[qb] += v[zb][qb];
         }
       }
 #pragma unroll
@@ -1688,15 +1692,23 @@ const CfgEntry kCfgs[] = {
 };
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
-// ---- split-K workspace, one per (device, stream) ------------------------------
-// Fixed capacity: INFEROP_SPLITK_WS_BYTES of fp32 partials and
-// INFEROP_SPLITK_WS_COUNTERS arrival counters, allocated at a stream's first
-// split-K call and kept until the process ends -- never grown, replaced or
-// freed, so a HIP graph captured on the stream keeps valid pointers and no
-// call waits for the host.  The automatic tile choice stays within the
-// capacity; a forced split that needs more is rejected before any launch.
-// The counters start at zero and every launch leaves them at zero (the
-// workgroup that completes a tile resets its counter).
+// ---- split-K workspace: a fixed pool of slots per device ---------------------
+// A slot holds INFEROP_SPLITK_WS_BYTES of fp32 partials and
+// INFEROP_SPLITK_WS_COUNTERS arrival counters.  Each device has
+// INFEROP_SPLITK_WS_SLOTS of them; a stream takes the next free slot of its
+// device at its first split-K call (the slot's memory is allocated then) and
+// keeps it until the process ends -- never grown, replaced, freed or handed to
+// another stream, so a HIP graph captured on the stream keeps valid pointers,
+// two streams never share partials, and no call waits for the host.  Once a
+// device's slots are all taken, further streams get no workspace: the
+// automatic tile choice then runs unsplit (inferop_hip_splitk_reserve), and
+// a forced split is rejected.  So a process holds at most
+// INFEROP_SPLITK_WS_SLOTS x (64 MiB + 64 KiB) per device, however many
+// streams it creates and destroys (a new stream at a destroyed stream's
+// address finds that stream's slot).  The automatic tile choice stays within
+// a slot's capacity; a forced split that needs more is rejected before any
+// launch.  The counters start at zero and every launch leaves them at zero
+// (the workgroup that completes a tile resets its counter).
 
 __global__ void fill_zero_kernel(int* p, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -1713,23 +1725,34 @@ struct Workspace {
   int* counters;
 };
 
-std::mutex g_ws_mutex;
-std::unordered_map<uint64_t, Workspace> g_ws;  // entries are never changed or erased
-hipStream_t g_zero_stream[64];                 // per device, for captured first calls
+struct WorkspacePool {
+  Workspace slot[INFEROP_SPLITK_WS_SLOTS];
+  hipStream_t owner[INFEROP_SPLITK_WS_SLOTS];
+  int used;  // slots handed out, in order; entries are never changed afterwards
+};
 
+std::mutex g_ws_mutex;
+WorkspacePool g_ws[64];         // per device ordinal
+hipStream_t g_zero_stream[64];  // per device, for captured first calls
+
+// The workspace of stream st on the current device: its slot, or the next
+// free one (allocated and its counters zeroed here).  hipErrorOutOfMemory
+// when every slot belongs to another stream.
 hipError_t get_workspace(hipStream_t st, float** ws, int** cnt) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
-  const uint64_t key = (uint64_t)(uintptr_t)st * 64u + (uint64_t)dev;
   std::lock_guard<std::mutex> lock(g_ws_mutex);
-  auto it = g_ws.find(key);
-  if (it != g_ws.end()) {
-    *ws = it->second.partials;
-    *cnt = it->second.counters;
-    return hipSuccess;
+  WorkspacePool& pool = g_ws[dev];
+  for (int i = 0; i < pool.used; ++i) {
+    if (pool.owner[i] == st) {
+      *ws = pool.slot[i].partials;
+      *cnt = pool.slot[i].counters;
+      return hipSuccess;
+    }
   }
+  if (pool.used >= INFEROP_SPLITK_WS_SLOTS) return hipErrorOutOfMemory;
   // First split-K call on this stream.  While the stream is being captured,
   // hipMalloc is only allowed in relaxed capture mode, and the counters are
   // zeroed on a library stream that is not captured (waited for here, once);
@@ -1760,9 +1783,14 @@ hipError_t get_workspace(hipStream_t st, float** ws, int** cnt) {
     const hipError_t e2 = hipThreadExchangeStreamCaptureMode(&mode);
     if (e == hipSuccess) e = e2;
   }
-  // a failed set-up keeps its memory (it may be in use by a launched fill)
-  if (e != hipSuccess) return e;
-  g_ws.emplace(key, Workspace{reinterpret_cast<float*>(base), counters});
+  if (e != hipSuccess) {
+    // a failed set-up keeps its memory (it may be in use by a launched fill)
+    // but takes no slot
+    return e;
+  }
+  pool.slot[pool.used] = Workspace{reinterpret_cast<float*>(base), counters};
+  pool.owner[pool.used] = st;
+  ++pool.used;
   *ws = reinterpret_cast<float*>(base);
   *cnt = counters;
   return hipSuccess;
@@ -1785,8 +1813,11 @@ hipError_t g_scratch_err[64];
 char* g_scratch_ptr[64];
 
 // The current device's scratch address, looked up on the first call on that
-// device (which also zeroes the counters on that call's stream, ahead of its
-// GEMM; afterwards every launch leaves them at zero).
+// device, which also zeroes the counters ahead of its GEMM (afterwards every
+// launch leaves them at zero): on that call's stream, or -- when the first
+// call is being captured -- on the library's own stream in relaxed capture
+// mode, waited for here, so the zeroing is never a node of the caller's graph
+// and eager calls before any replay find the counters at zero too.
 hipError_t get_scratch(hipStream_t st, float** ws, int** cnt) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -1795,22 +1826,27 @@ hipError_t get_scratch(hipStream_t st, float** ws, int** cnt) {
   std::call_once(g_scratch_once[dev], [&] {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     hipError_t r = hipStreamIsCapturing(st, &cs);
-    // under capture the symbol lookup (which may load the code object) runs in
-    // relaxed capture mode; the zeroing kernel becomes part of the graph
     hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
     const bool capturing = r == hipSuccess && cs != hipStreamCaptureStatusNone;
     if (capturing) r = hipThreadExchangeStreamCaptureMode(&mode);
     void* ptr = nullptr;
     if (r == hipSuccess) r = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-    if (capturing) {
-      const hipError_t r2 = hipThreadExchangeStreamCaptureMode(&mode);
-      if (r == hipSuccess) r = r2;
-    }
     if (r == hipSuccess && ptr == nullptr) r = hipErrorInvalidSymbol;
     if (r == hipSuccess) {
       g_scratch_ptr[dev] = static_cast<char*>(ptr);
-      r = launch_fill_zero(reinterpret_cast<int*>(g_scratch_ptr[dev] + INFEROP_SPLITK_WS_BYTES),
-                           INFEROP_SPLITK_WS_COUNTERS, st);
+      int* counters = reinterpret_cast<int*>(g_scratch_ptr[dev] + INFEROP_SPLITK_WS_BYTES);
+      if (capturing) {
+        std::lock_guard<std::mutex> lock(g_ws_mutex);  // guards g_zero_stream
+        if (!g_zero_stream[dev]) r = hipStreamCreateWithFlags(&g_zero_stream[dev], hipStreamNonBlocking);
+        if (r == hipSuccess) r = launch_fill_zero(counters, INFEROP_SPLITK_WS_COUNTERS, g_zero_stream[dev]);
+        if (r == hipSuccess) r = hipStreamSynchronize(g_zero_stream[dev]);
+      } else {
+        r = launch_fill_zero(counters, INFEROP_SPLITK_WS_COUNTERS, st);
+      }
+    }
+    if (capturing) {
+      const hipError_t r2 = hipThreadExchangeStreamCaptureMode(&mode);
+      if (r == hipSuccess) r = r2;
     }
     g_scratch_err[dev] = r;
   });
@@ -1847,10 +1883,16 @@ PersistPlan persist_plan(const CfgEntry& cf, int64_t tiles, int64_t kg, int64_t 
 
 // Workspace a launch of configuration cf with `split` K partitions needs
 // (0 without a split), and whether it fits the fixed capacity.
+// A tile's partial is laid out in 16x16 output blocks of 1 KB (the fixup's
+// pairs): an 8-row activation tile (the M <= 8 wide decode configurations)
+// still takes whole 16-row blocks.
+int64_t tile_partial_bytes(const CfgEntry& cf) {
+  return (int64_t)((cf.bm + 15) / 16) * 16 * cf.bn * 4;
+}
 int64_t workspace_bytes(const CfgEntry& cf, int64_t split, int64_t m, int64_t n) {
   if (split <= 1 || cf.kind == 3) return 0;
   const int64_t tiles = ((n + cf.bn - 1) / cf.bn) * ((m + cf.bm - 1) / cf.bm);
-  return split * tiles * cf.bn * cf.bm * 4;
+  return split * tiles * tile_partial_bytes(cf);
 }
 bool workspace_fits(const CfgEntry& cf, int64_t split, int64_t m, int64_t n) {
   if (split <= 1 || cf.kind == 3) return true;
@@ -1921,6 +1963,19 @@ extern "C" int64_t inferop_hip_gemm_workspace_bytes(int32_t cfg, int32_t split, 
   const int64_t tiles = ((n + cf.bn - 1) / cf.bn) * ((m + cf.bm - 1) / cf.bm);
   if (s > 1 && cf.kind != 3 && tiles > INFEROP_SPLITK_WS_COUNTERS) return -1;
   return workspace_bytes(cf, s, m, n);
+}
+
+extern "C" int inferop_hip_splitk_reserve(void* stream) {
+  float* ws = nullptr;
+  int* cnt = nullptr;
+  return get_workspace(static_cast<hipStream_t>(stream), &ws, &cnt);
+}
+
+extern "C" int inferop_hip_splitk_slots_used(void) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return -1;
+  std::lock_guard<std::mutex> lock(g_ws_mutex);
+  return g_ws[dev].used;
 }
 
 namespace inferop_hip {
