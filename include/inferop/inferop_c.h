@@ -136,16 +136,27 @@ int inferop_w8a8_block_fp8_grouped_gemm_masked(void* c, const void* a_q, const v
 /* --- tuning and testing (no counterpart in the reference) ---
  * The GEMM with an explicit kernel configuration and split-K factor instead
  * of the automatic gfx950 choice.  config in [0, inferop_gemm_num_configs()).
- * The persistent configurations ("per_" names) take whole tiles (split_k is
- * ignored) and need an even K / 128; other K return INFEROP_ERR_ARGUMENT. */
+ * The persistent configurations ("per_" names) cut the tiles of their last,
+ * partial round into split_k K ranges and need an even K / 128; other K
+ * return INFEROP_ERR_ARGUMENT.  A split whose partials exceed a workspace
+ * slot, or on a stream that can take no slot, returns INFEROP_ERR_ARGUMENT. */
 int inferop_gemm_num_configs(void);
 const char* inferop_gemm_config_name(int config);
 int inferop_w8a8_block_fp8_gemm_config(void* c, const void* a_q, const void* a_scales,
                                        const void* b_q, const void* b_scales, int64_t m,
                                        int64_t n, int64_t k, int32_t out_dt, int32_t config,
                                        int32_t split_k, void* stream);
-/* The configuration and split-K factor the automatic choice would use. */
+/* The configuration and split-K factor the automatic choice would use (on a
+ * stream that has, or can still take, a split-K workspace slot). */
 int inferop_gemm_select(int64_t m, int64_t n, int64_t k, int32_t* config, int32_t* split_k);
+/* Split-K workspace of the current device: a fixed pool of *slots_total
+ * slots of *slot_bytes each (fp32 partials plus arrival counters), of which
+ * *slots_used are held by streams.  A stream takes a slot at its first
+ * split-K call and keeps it until the process ends; once all are held, the
+ * automatic choice runs later streams' GEMMs unsplit and
+ * inferop_w8a8_block_fp8_gemm_config with a split returns
+ * INFEROP_ERR_ARGUMENT on them.  Any pointer may be NULL. */
+int inferop_splitk_workspace_info(int32_t* slots_used, int32_t* slots_total, int64_t* slot_bytes);
 /* The grouped GEMM with an explicit configuration: one of the tiled
  * configurations with a grouped variant (others return INFEROP_ERR_ARGUMENT);
  * and the configuration the automatic choice would use. */

@@ -54,6 +54,8 @@ C_API = [
      [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i32, _vp]),
     ("inferop_gemm_select", ctypes.c_int,
      [_i64, _i64, _i64, ctypes.POINTER(_i32), ctypes.POINTER(_i32)]),
+    ("inferop_splitk_workspace_info", ctypes.c_int,
+     [ctypes.POINTER(_i32), ctypes.POINTER(_i32), ctypes.POINTER(_i64)]),
     ("inferop_selftest_fp8_codec", ctypes.c_int, [_u64, _u64, _vp, _vp]),
     ("inferop_diag_read_stream", ctypes.c_int, [_vp, _i64, _i32, _vp, _vp]),
     ("inferop_diag_mfma_loop", ctypes.c_int, [_i32, _i32, _i32, _vp, _vp]),

@@ -65,11 +65,21 @@ typedef struct {
   int32_t grouped; /* kind 2: has a grouped-expert variant */
 } inferop_gemm_cfg_info;
 
-/* Capacity of the split-K workspace the library keeps per (device, stream):
- * fp32 partial bytes and arrival counters (one per output tile).  A launch
- * whose split needs more is rejected with hipErrorInvalidValue. */
+/* Capacity of one split-K workspace slot: fp32 partial bytes and arrival
+ * counters (one per output tile).  A launch whose split needs more is
+ * rejected with hipErrorInvalidValue.  Each device has
+ * INFEROP_SPLITK_WS_SLOTS slots, handed out one per stream at the stream's
+ * first split-K call and kept by it until the process ends. */
 #define INFEROP_SPLITK_WS_BYTES (64ll << 20)
 #define INFEROP_SPLITK_WS_COUNTERS 16384
+#define INFEROP_SPLITK_WS_SLOTS 8
+
+/* Takes (or finds) the current device's workspace slot of `stream`, allocating
+ * it on the stream's first use.  0 on success; hipErrorOutOfMemory when every
+ * slot belongs to another stream (the caller then launches unsplit). */
+int inferop_hip_splitk_reserve(void* stream);
+/* Slots of the current device handed out so far. */
+int inferop_hip_splitk_slots_used(void);
 
 int inferop_hip_gemm_num_configs(void);
 int inferop_hip_gemm_config_info(int32_t cfg, inferop_gemm_cfg_info* info);

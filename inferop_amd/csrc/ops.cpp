@@ -420,9 +420,9 @@ GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
   return {kPreN128M128S2, int32_t(split)};
 }
 
-// The automatic choice with its K split reduced, where needed, to what the
-// split-K workspace the library keeps per stream holds (a long K on the
-// decode kernels would otherwise ask for one partial tile per few groups).
+// The automatic choice with its K split reduced, where needed, to what one
+// split-K workspace slot holds (a long K on the decode kernels would otherwise
+// ask for one partial tile per few groups).
 GemmChoice choose_gemm(int64_t m, int64_t n, int64_t k, int cus) {
   GemmChoice ch = select_gemm(m, n, k, cus);
   while (ch.split > 1) {
@@ -431,6 +431,17 @@ GemmChoice choose_gemm(int64_t m, int64_t n, int64_t k, int cus) {
     const int64_t s = b < 0 ? 1 : (int64_t)ch.split * INFEROP_SPLITK_WS_BYTES / b;
     ch.split = int32_t(s < ch.split ? (s < 1 ? 1 : s) : ch.split - 1);
   }
+  return ch;
+}
+
+// The choice for a launch on `stream`: a split that needs workspace takes the
+// stream's slot (its first split-K call allocates it); when the device has no
+// slot left for this stream, the same configuration runs unsplit.
+GemmChoice choose_gemm_on(int64_t m, int64_t n, int64_t k, int cus, void* stream) {
+  GemmChoice ch = choose_gemm(m, n, k, cus);
+  if (ch.split > 1 && inferop_hip_gemm_workspace_bytes(ch.cfg, ch.split, m, n, k) > 0 &&
+      inferop_hip_splitk_reserve(stream) != 0)
+    ch.split = 1;
   return ch;
 }
 
@@ -499,7 +510,7 @@ int rmsnorm_quant_impl(void* residual, void* q, void* scales, const void* x, con
 
 int topk_impl(int32_t* ids, void* weights, const void* logits, int32_t tokens, int32_t experts,
               int32_t topk, int32_t renormalize, void* stream) {
-  // reference moe/topk_softmax.cu:104-108 guard
+  // reference moe/topk_softmax.cu:89-92 guard
   if (tokens <= 0 || experts <= 0 || experts > 1024 || topk <= 0 || topk > experts)
     return INFEROP_ERR_SHAPE;
   if (!current_device()) return INFEROP_ERR_DEVICE;
@@ -550,7 +561,7 @@ int gemm_impl(void* c, const void* a_q, const void* a_scales, const void* b_q,
   if (!valid_input_dtype(out_dt)) return INFEROP_ERR_DTYPE;  // reference :185-186 silent no-op
   const DeviceEntry* d = gemm_device();
   if (!d) return INFEROP_ERR_DEVICE;
-  const GemmChoice ch = choose_gemm(m, n, k, d->cus);
+  const GemmChoice ch = choose_gemm_on(m, n, k, d->cus, stream);
   return gemm_launch(c, a_q, a_scales, b_q, b_scales, m, n, k, out_dt, ch.cfg, ch.split, stream);
 }
 
@@ -851,6 +862,9 @@ extern "C" int inferop_w8a8_block_fp8_gemm_config(void* c, const void* a_q, cons
   const int64_t ws = inferop_hip_gemm_workspace_bytes(config, split_k, m, n, k);
   if (ws < 0 || ws > INFEROP_SPLITK_WS_BYTES) return INFEROP_ERR_ARGUMENT;
   if (!gemm_device()) return INFEROP_ERR_DEVICE;
+  // a split needs the stream's workspace slot; none left on the device for
+  // this stream is an argument error (nothing is launched)
+  if (ws > 0 && inferop_hip_splitk_reserve(stream) != 0) return INFEROP_ERR_ARGUMENT;
   return gemm_launch(c, a_q, a_scales, b_q, b_scales, m, n, k, out_dt, config, split_k, stream);
 }
 
@@ -918,6 +932,17 @@ extern "C" int inferop_grouped_gemm_masked_select(int64_t max_m, int64_t n, int6
     return INFEROP_ERR_ARGUMENT;
   const int64_t rows = expected_m > 0 ? (expected_m < max_m ? expected_m : max_m) : max_m;
   *config = select_grouped(rows * num_experts, num_experts * max_m, k, num_experts);
+  return INFEROP_OK;
+}
+
+extern "C" int inferop_splitk_workspace_info(int32_t* slots_used, int32_t* slots_total,
+                                             int64_t* slot_bytes) {
+  if (!current_device()) return INFEROP_ERR_DEVICE;
+  const int used = inferop_hip_splitk_slots_used();
+  if (used < 0) return INFEROP_ERR_LAUNCH;
+  if (slots_used) *slots_used = used;
+  if (slots_total) *slots_total = INFEROP_SPLITK_WS_SLOTS;
+  if (slot_bytes) *slot_bytes = INFEROP_SPLITK_WS_BYTES + 4ll * INFEROP_SPLITK_WS_COUNTERS;
   return INFEROP_OK;
 }
 

@@ -983,6 +983,9 @@ hipError_t silu_device_cus(int* cus) {
 // us; four steps in flight per wave (94 VGPRs, 5 waves per SIMD) 100 us.
 constexpr int kSiluLdsWgPerCu = 4;
 
+// The LDS-table kernels take the group count and d as 32-bit values and form
+// column offsets (group * 128) in 32 bits: they run only for ngroups < 2^32
+// and d < 2^31; anything larger takes the 64-bit kernel below them.
 template <int DT>
 hipError_t launch_silu_mul_quant(uint8_t* q, float* scales, const void* gate_up, int64_t tokens,
                                  int64_t d, hipStream_t st) {
@@ -995,7 +998,7 @@ hipError_t launch_silu_mul_quant(uint8_t* q, float* scales, const void* gate_up,
       constexpr int kStep = NT / 16 * UL;
       int cus = 0;
       if (hipError_t e = silu_device_cus(&cus); e != hipSuccess) return e;
-      if (ngroups >= (int64_t)kStep * cus && ngroups <= 0xFFFFFFFFll) {
+      if (ngroups >= (int64_t)kStep * cus && ngroups <= 0xFFFFFFFFll && d <= 0x7FFFFFFF) {
         const int64_t steps = (ngroups + kStep - 1) / kStep;
         const int64_t blocks = steps < (int64_t)cus * kWgPerCu ? steps : (int64_t)cus * kWgPerCu;
         hipLaunchKernelGGL((silu_mul_quant_lds_kernel<kFp16, UL, NT>), dim3((unsigned)blocks),
@@ -1011,7 +1014,7 @@ hipError_t launch_silu_mul_quant(uint8_t* q, float* scales, const void* gate_up,
     constexpr int kStep = NT / 16 * UL;  // groups per workgroup step
     int cus = 0;
     if (hipError_t e = silu_device_cus(&cus); e != hipSuccess) return e;
-    if (ngroups >= (int64_t)kStep * cus && ngroups <= 0xFFFFFFFFll) {
+    if (ngroups >= (int64_t)kStep * cus && ngroups <= 0xFFFFFFFFll && d <= 0x7FFFFFFF) {
       const int64_t steps = (ngroups + kStep - 1) / kStep;
       const int64_t blocks = steps < (int64_t)cus * kSiluLdsWgPerCu ? steps
                                                                      : (int64_t)cus * kSiluLdsWgPerCu;

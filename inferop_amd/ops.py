@@ -181,6 +181,17 @@ def gemm_select(m: int, n: int, k: int):
     return cfg.value, split.value
 
 
+def splitk_workspace_info():
+    """(slots_used, slots_total, slot_bytes) of the current device's split-K
+    workspace pool."""
+    used, total, nbytes = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64()
+    st = lib().inferop_splitk_workspace_info(ctypes.byref(used), ctypes.byref(total),
+                                             ctypes.byref(nbytes))
+    if st != Status.OK:
+        raise InferopError(st, "splitk_workspace_info")
+    return used.value, total.value, nbytes.value
+
+
 def w8a8_block_fp8_gemm_config(c, a_q, a_scales, b_q, b_scales, m: int, n: int, k: int,
                                out_dt, config: int, split_k: int = 1, stream=None) -> int:
     return lib().inferop_w8a8_block_fp8_gemm_config(

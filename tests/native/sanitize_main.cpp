@@ -99,6 +99,17 @@ int64_t inferop_hip_gemm_workspace_bytes(int32_t cfg, int32_t split, int64_t m, 
   if (tiles > (int64_t(1) << 40) / (s * 65536)) return -1;
   return s * tiles * 65536;
 }
+// the workspace pool: INFEROP_SPLITK_WS_SLOTS streams take a slot each
+void* g_slot_owner[INFEROP_SPLITK_WS_SLOTS];
+int g_slots_used = 0;
+int inferop_hip_splitk_reserve(void* stream) {
+  for (int i = 0; i < g_slots_used; ++i)
+    if (g_slot_owner[i] == stream) return 0;
+  if (g_slots_used >= INFEROP_SPLITK_WS_SLOTS) return 2;  // hipErrorOutOfMemory
+  g_slot_owner[g_slots_used++] = stream;
+  return 0;
+}
+int inferop_hip_splitk_slots_used(void) { return g_slots_used; }
 static int gemm_stub(const inferop_gemm_launch* l, int64_t m, int64_t n, int64_t k, int32_t dt) {
   check(l && l->cfg >= 0 && l->cfg < kStubConfigs, "gemm config in range");
   check(l && l->split_k >= 1 && l->split_k <= k / 128, "gemm split in range");
@@ -220,6 +231,35 @@ void host_layer() {
   check(inferop_w8a8_block_fp8_gemm_config(d, d, d, d, d, 4096, 4096, 4096, 2, 8, 64, nullptr) ==
             INFEROP_ERR_ARGUMENT,
         "forced split beyond the workspace");
+  // workspace slots: once every slot belongs to a stream, a further stream's
+  // automatic choice runs unsplit and a forced split on it is rejected
+  {
+    int32_t cfg = -1, split = -1;
+    check(inferop_gemm_select(64, 2112, 7168, &cfg, &split) == INFEROP_OK && split > 1,
+          "a split shape");
+    char streams[INFEROP_SPLITK_WS_SLOTS + 1];
+    for (int i = 0; i <= INFEROP_SPLITK_WS_SLOTS; ++i) {
+      g_last_split = -1;
+      check(inferop_w8a8_block_fp8_gemm(d, d, d, d, d, 64, 2112, 7168, 128, 128, 2,
+                                        &streams[i]) == INFEROP_OK,
+            "gemm on a new stream");
+      const bool has_slot = i < INFEROP_SPLITK_WS_SLOTS - 1;  // the null stream holds one
+      check(g_last_cfg == cfg && g_last_split == (has_slot ? split : 1), "split only with a slot");
+    }
+    int32_t used = -1, total = -1;
+    int64_t bytes = -1;
+    check(inferop_splitk_workspace_info(&used, &total, &bytes) == INFEROP_OK &&
+              used == INFEROP_SPLITK_WS_SLOTS && total == INFEROP_SPLITK_WS_SLOTS &&
+              bytes == INFEROP_SPLITK_WS_BYTES + 4 * INFEROP_SPLITK_WS_COUNTERS,
+          "workspace info");
+    check(inferop_w8a8_block_fp8_gemm_config(d, d, d, d, d, 64, 2112, 7168, 2, cfg, 2,
+                                             &streams[INFEROP_SPLITK_WS_SLOTS]) ==
+              INFEROP_ERR_ARGUMENT,
+          "forced split without a slot");
+    check(inferop_w8a8_block_fp8_gemm_config(d, d, d, d, d, 64, 2112, 7168, 2, cfg, 2, nullptr) ==
+              INFEROP_OK,
+          "forced split with a slot");
+  }
   check(inferop_diag_read_stream(d, 8, 1, d, nullptr) == INFEROP_ERR_ARGUMENT, "read 8 bytes");
   check(inferop_diag_stripe_read(d, 4096, 3072, 0, 0, d, nullptr) == INFEROP_ERR_ARGUMENT,
         "stripe read k");

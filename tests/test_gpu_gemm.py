@@ -59,8 +59,13 @@ def test_config1_decode_full_parity(m, nk):
     device()
     n, k = nk
     print(f"config1 m={m} n={n} k={k}", flush=True)
-    _, aq, as_, bq, bs = _host_case(m, n, k, seed=100 + m)
-    c = _gemm(to_dev(aq), to_dev(as_), to_dev(bq), to_dev(bs), m, n, k)
+    a_bits, aq, as_, bq, bs = _host_case(m, n, k, seed=100 + m)
+    # the decode step as the caller runs it: GPU quantizer (every byte and
+    # scale equal to the oracle's), then the GEMM on its outputs
+    q, s = inferop_amd.quantize(bf16_dev(a_bits))
+    assert np.array_equal(to_np(q), aq)
+    assert np.array_equal(to_np(s).view(np.uint32), as_.view(np.uint32))
+    c = _gemm(q, s, to_dev(bq), to_dev(bs), m, n, k)
     assert_gemm_close(out_to_f32(c), oracle.gemm(aq, as_, bq, bs), f"config1 {m}x{n}x{k}")
 
 
@@ -155,13 +160,17 @@ def _device_case(m, n, k, seed):
 def _check_full(a, aq, as_, bq, bs, outs, rows, what):
     """Every element of every output in `outs` against the float64 GPU
     reference; the reference is first checked against the oracle
-    (reference.cpp:93-110) on the sampled rows, and the GPU quantizer's bytes
-    and scales on those rows against the oracle's quantizer."""
+    (reference.cpp:93-110) on the sampled rows.  The GPU quantizer's bytes
+    and scales are compared with the oracle's quantizer (reference.cpp:65-80)
+    over the whole activation tensor, every byte and every scale (the
+    reference's own test compares every byte, tests/test_quant.cpp:62-63)."""
+    qr, sr = oracle.quant(datagen.bf16_bits_to_f32(to_np(a)))
+    q_all, s_all = to_np(aq), to_np(as_)
+    nq = int((q_all != qr).sum())
+    ns = int((s_all.view(np.uint32) != sr.view(np.uint32)).sum())
+    assert nq == 0 and ns == 0, f"{what}: quantizer differs in {nq} bytes, {ns} scales"
+    del qr, sr, q_all, s_all
     aq_h, as_h = to_np(aq[rows]), to_np(as_[rows])
-    # the GPU quantizer's rows equal the oracle's on the same bf16 inputs
-    qr, sr = oracle.quant(datagen.bf16_bits_to_f32(to_np(a[rows])))
-    assert np.array_equal(aq_h, qr), what
-    assert np.array_equal(as_h.view(np.uint32), sr.view(np.uint32)), what
     want = oracle.gemm_rows(aq_h, as_h, to_np(bq), to_np(bs), np.arange(len(rows)))
     ref = gemm_ref_f64(aq, as_, bq, bs)
     anchor_ref_rows(ref, want, rows, what)

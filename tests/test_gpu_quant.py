@@ -110,9 +110,9 @@ def test_quant_rejected_shapes_leave_outputs_untouched():
 
 
 @pytest.mark.gpu
-def test_quant_large_sampled_rows_and_roundtrip():
-    # M=4096, K=16384 (config 2's largest K): rows sampled against the oracle,
-    # the whole tensor checked by a size-independent round-trip bound
+def test_quant_large_whole_tensor_and_roundtrip():
+    # M=4096, K=16384 (config 2's largest K): every byte and scale against the
+    # oracle, and the size-independent round-trip bound on top
     device()
     m, k = 4096, 16384
     g = torch.Generator(device="cuda:0").manual_seed(3)
@@ -120,10 +120,9 @@ def test_quant_large_sampled_rows_and_roundtrip():
     q = torch.empty((m, k), dtype=torch.uint8, device="cuda:0")
     s = torch.empty((m, k // 128), dtype=torch.float32, device="cuda:0")
     assert inferop_amd.quant_fp8_per_token_group(q, s, x, DT.bf16, m, k) == 0
-    rows = np.array([0, 1, 2047, 4095] + list(np.random.default_rng(1).integers(0, m, 12)))
-    xs = to_np(x[rows]).view(np.uint16)
-    qr, sr = oracle.quant(datagen.bf16_bits_to_f32(xs))
-    _assert_same(to_np(q[rows]), to_np(s[rows]), qr, sr, "4096x16384 sampled rows")
+    qr, sr = oracle.quant(datagen.bf16_bits_to_f32(to_np(x).view(np.uint16)))
+    _assert_same(to_np(q), to_np(s), qr, sr, "4096x16384 whole tensor")
+    del qr, sr
     # dequantize on the GPU and bound the error everywhere
     xd = torch.empty((m, k), dtype=torch.float32, device="cuda:0")
     assert inferop_amd.dequant_fp8_per_token_group(xd, DT.fp32, q, s, m, k) == 0

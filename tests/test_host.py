@@ -2,6 +2,7 @@
 symbol the headers declare, the drop-in C++ API links against a program built
 from the reference's own ops.h, and argument guards behave like the
 reference (nothing is launched without a device)."""
+import ctypes
 import os
 import re
 import shutil
@@ -329,9 +330,49 @@ def _tile_of(name):
         return 16, 16
     if name.startswith("dec_m"):
         return 16, int(name.split("_")[1][1:])
+    if name.startswith("dw_m"):  # one 16-row weight stripe, bm activation rows
+        return 16, int(name.split("_m")[1].split("_")[0])
     bn = int(name.split("_n")[1].split("_")[0])
     bm = int(name.split("_m")[1].split("_")[0])
     return bn, bm
+
+
+def _workspace_bytes(cfg, split, m, n, k):
+    f = inferop_amd.lib().inferop_hip_gemm_workspace_bytes
+    f.restype = ctypes.c_int64
+    f.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64]
+    return f(cfg, split, m, n, k)
+
+
+def test_workspace_bytes_per_tile_of_every_split_configuration():
+    # a tile's partial is stored as whole 16x16 blocks of 1 KB (the fixup's
+    # layout): bn * ceil(bm / 16) * 16 * 4 bytes per tile and split, also for
+    # the 8-row activation tiles, whose partial still fills 16-row blocks
+    names = [inferop_amd.gemm_config_name(i) for i in range(inferop_amd.gemm_num_configs())]
+    m, n, k, split = 40, 1000, 7168, 3
+    for cfg, name in enumerate(names):
+        if name.startswith("per_"):
+            continue
+        bn, bm = _tile_of(name)
+        tiles = -(-n // bn) * -(-m // bm)
+        want = split * tiles * bn * (-(-bm // 16) * 16) * 4
+        assert _workspace_bytes(cfg, split, m, n, k) == want, name
+        assert _workspace_bytes(cfg, 1, m, n, k) == 0, name
+    m8 = names.index("dw_m8_k8_w4a4")
+    assert _workspace_bytes(m8, 32, 1, 65536, 7168) == 32 * 4096 * 1024
+
+
+def test_forced_split_of_8_row_tiles_beyond_workspace_is_rejected():
+    # m=1, n=65536, split 32 on the 8-row wide decode tiles needs 128 MiB of
+    # partials (4096 stripes x 1 KB x 32), twice a workspace slot
+    S = inferop_amd.Status
+    names = [inferop_amd.gemm_config_name(i) for i in range(inferop_amd.gemm_num_configs())]
+    g = inferop_amd.w8a8_block_fp8_gemm_config
+    for name in ("dw_m8_k8_w4a4", "dw_m8_k4_w4a4"):
+        cfg = names.index(name)
+        assert g(0, 0, 0, 0, 0, 1, 65536, 7168, inferop_amd.dtype.bf16, cfg, 32) == S.ERR_ARGUMENT
+        # 16 splits need exactly the 64 MiB: not rejected for the workspace
+        assert g(0, 0, 0, 0, 0, 1, 65536, 7168, inferop_amd.dtype.bf16, cfg, 16) != S.ERR_ARGUMENT
 
 
 def test_automatic_split_fits_the_fixed_workspace():
@@ -344,9 +385,10 @@ def test_automatic_split_fits_the_fixed_workspace():
                              (512, 1 << 20), (7168, 1 << 24), (64, 1 << 24))]
     for (m, n, k) in shapes:
         cfg, split = inferop_amd.gemm_select(m, n, k)
-        if split == 1 or names[cfg].startswith("dw_"):
+        if split == 1:
             continue
         bn, bm = _tile_of(names[cfg])
+        bm = -(-bm // 16) * 16  # partials in whole 16-row blocks
         tiles = -(-n // bn) * -(-m // bm)
         if names[cfg].startswith("per_"):
             # persistent tiles: only the last, partial round's tiles are cut,

@@ -5,6 +5,9 @@ outputs must be identical bit for bit -- on two calls in a row, the second
 smaller, so the second runs on the scratch the first left behind -- and
 within the GEMM tolerance of the oracle."""
 import ctypes
+import os
+import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -66,3 +69,97 @@ def test_noalloc_gemm_guards_match():
     assert noalloc(*p, 4, 8, 128, 128, 128, int(DT.fp8_e4m3), None) == S.ERR_DTYPE
     torch.cuda.synchronize()
     assert (c == 5.0).all()
+
+
+@pytest.mark.gpu
+def test_noalloc_split_k_graph_replays_match_eager():
+    # a captured split-K no-alloc call (64 x 2112 x 7168: 128x32 tiles, K in
+    # 3) replays bit-identically to the eager call, with eager no-alloc calls
+    # of another shape between the replays (they leave the counters at zero)
+    device()
+    m, n, k = 64, 2112, 7168
+    assert inferop_amd.gemm_select(m, n, k)[1] > 1
+    _, a_f32, bq, bs = datagen.gemm_case(m, n, k, seed=77)
+    aq, as_ = oracle.quant(a_f32)
+    args = [to_dev(v) for v in (aq, as_, bq, bs)]
+    o_m, o_n, o_k = 33, 1024, 7168
+    _, o_f32, obq, obs = datagen.gemm_case(o_m, o_n, o_k, seed=78)
+    oaq, oas = oracle.quant(o_f32)
+    oargs = [to_dev(v) for v in (oaq, oas, obq, obs)]
+    st = torch.cuda.Stream()
+    want = torch.empty((m, n), dtype=torch.bfloat16, device="cuda:0")
+    got = torch.empty_like(want)
+    other = torch.empty((o_m, o_n), dtype=torch.bfloat16, device="cuda:0")
+    with torch.cuda.stream(st):
+        assert inferop_amd.w8a8_block_fp8_gemm_noalloc(want, *args, m, n, k,
+                                                       stream=st.cuda_stream) == 0
+    st.synchronize()
+    assert_gemm_close(want.float().cpu().numpy(), oracle.gemm(aq, as_, bq, bs), "eager")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        assert inferop_amd.w8a8_block_fp8_gemm_noalloc(got, *args, m, n, k,
+                                                       stream=st.cuda_stream) == 0
+    for rep in range(3):
+        got.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"replay {rep}"
+        with torch.cuda.stream(st):
+            assert inferop_amd.w8a8_block_fp8_gemm_noalloc(other, *oargs, o_m, o_n, o_k,
+                                                           stream=st.cuda_stream) == 0
+        st.synchronize()
+
+
+_NOALLOC_FIRST_CALL_CAPTURED = r"""
+import sys
+import torch
+import inferop_amd
+m, n, k = 64, 2112, 7168
+g = torch.Generator(device="cuda:0").manual_seed(11)
+a = torch.randn((m, k), generator=g, device="cuda:0").to(torch.bfloat16)
+aq, as_ = inferop_amd.quantize(a)
+bq = (torch.randn((n, k), generator=g, device="cuda:0") * 0.3).to(torch.float8_e4m3fn)
+bq = bq.view(torch.uint8)
+bs = torch.rand(((n + 127) // 128, k // 128), generator=g, device="cuda:0") * 0.01 + 1e-3
+assert inferop_amd.gemm_select(m, n, k)[1] > 1
+torch.cuda.synchronize()
+st = torch.cuda.Stream()
+got = torch.empty((m, n), dtype=torch.bfloat16, device="cuda:0")
+graph = torch.cuda.CUDAGraph()
+# the process's first no-alloc call, inside the capture: the scratch address
+# is looked up and its counters zeroed outside the graph
+with torch.cuda.graph(graph, stream=st):
+    assert inferop_amd.w8a8_block_fp8_gemm_noalloc(got, aq, as_, bq, bs, m, n, k,
+                                                   stream=st.cuda_stream) == 0
+# an eager no-alloc call before any replay finds the counters at zero
+want = torch.empty_like(got)
+with torch.cuda.stream(st):
+    assert inferop_amd.w8a8_block_fp8_gemm_noalloc(want, aq, as_, bq, bs, m, n, k,
+                                                   stream=st.cuda_stream) == 0
+st.synchronize()
+plain = torch.empty_like(got)
+assert inferop_amd.w8a8_block_fp8_gemm(plain, aq, as_, bq, bs, m, n, k) == 0
+torch.cuda.synchronize()
+if not torch.equal(want, plain):
+    print("eager no-alloc call differs from the allocating entry point", flush=True)
+    sys.exit(1)
+for rep in range(3):
+    got.zero_(); torch.cuda.synchronize()
+    graph.replay(); torch.cuda.synchronize()
+    if not torch.equal(got, want):
+        print("replay", rep, "differs from eager", flush=True)
+        sys.exit(1)
+print("ok", flush=True)
+"""
+
+
+@pytest.mark.gpu
+def test_noalloc_first_call_captured_in_fresh_process():
+    # a child process, so that the captured call is its first no-alloc call
+    device()
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, PYTHONPATH=root + os.pathsep + os.environ.get("PYTHONPATH", ""))
+    r = subprocess.run([sys.executable, "-c", _NOALLOC_FIRST_CALL_CAPTURED], env=env,
+                       capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0 and "ok" in r.stdout, (r.stdout[-2000:], r.stderr[-2000:])
