@@ -79,6 +79,24 @@ int inferop_w8a8_block_fp8_gemm_noalloc(void* c, const void* a_q, const void* a_
                                         int64_t n, int64_t k, int32_t group_size,
                                         int32_t block_n, int32_t out_dt, void* stream);
 
+/* --- extension: the quantizer and the GEMM in one call (no counterpart in
+ * the reference; the pair quant_fp8_per_token_group, ops.h:64-65, then
+ * w8a8_block_fp8_gemm, ops.h:81-84), see inferop::quant_w8a8_block_fp8_gemm
+ * in ops.h.  x [m, k] in dt; q [m, k] and scales [m, k/128] receive exactly
+ * what inferop_quant_fp8_per_token_group writes (group 128) and c exactly what
+ * inferop_w8a8_block_fp8_gemm computes from them.  The GEMM's guards (with
+ * its diagnostic, INFEROP_ERR_SHAPE) and dt / out_dt outside {fp32, fp16,
+ * bf16} (INFEROP_ERR_DTYPE); nothing is written then.  One kernel launch
+ * where the GEMM's automatic choice is an unsplit 8-row decode configuration
+ * (m <= 8) with x 16-byte and q 8-byte aligned, else two. */
+int inferop_quant_w8a8_block_fp8_gemm(void* c, void* q, void* scales, const void* x, int32_t dt,
+                                      const void* b_q, const void* b_scales, int64_t m, int64_t n,
+                                      int64_t k, int32_t group_size, int32_t block_n,
+                                      int32_t out_dt, void* stream);
+/* Kernel launches that call makes for an m x n x k problem with aligned
+ * pointers (1 or 2; -1 for an invalid shape). */
+int inferop_quant_w8a8_block_fp8_gemm_launches(int64_t m, int64_t n, int64_t k);
+
 /* --- replaces ops.h:108-110 topk_softmax ---
  * tokens <= 0, num_experts <= 0, num_experts > 1024, topk <= 0 or
  * topk > num_experts return INFEROP_ERR_SHAPE and write nothing (the

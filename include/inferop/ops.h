@@ -108,6 +108,22 @@ void fused_add_rmsnorm_quant_fp8(void* residual, void* q, void* scales, const vo
                                  float eps = 1e-6f, int group_size = 128,
                                  void* stream = nullptr);
 
+// --- extension: the quantizer and the GEMM in one call ------------------------
+// No counterpart in the reference ops.h, whose decode step is two calls:
+// quant_fp8_per_token_group (ops.h:64-65) then w8a8_block_fp8_gemm
+// (ops.h:81-84) on its output.  This call writes the same q / scales and the
+// same C as that pair (group_size 128, the GEMM's automatic kernel choice),
+// bit for bit; up to 8 rows it is one kernel launch (the GEMM quantizes its
+// own activations), otherwise the two launches on the stream.
+//   x: [m, k] in dt (fp32 / fp16 / bf16);  q: [m, k] E4M3;  scales: [m, k/128]
+//   b_q, b_scales, c: as for w8a8_block_fp8_gemm
+// Shape checks and diagnostics as for the GEMM; an invalid dt or out_dt is a
+// silent no-op.
+void quant_w8a8_block_fp8_gemm(void* c, void* q, void* scales, const void* x, dtype dt,
+                               const void* b_q, const void* b_scales, int64_t m, int64_t n,
+                               int64_t k, int group_size = 128, int block_n = 128,
+                               dtype out_dt = dtype::bf16, void* stream = nullptr);
+
 // --- extension: grouped W8A8 blockwise-FP8 GEMM over MoE experts --------------
 // No counterpart in the reference ops.h: its roadmap lists the grouped GEMM
 // for MoE (docs/ROADMAP.md:39, "contiguous / masked layouts"); this is the

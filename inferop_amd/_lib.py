@@ -32,6 +32,9 @@ C_API = [
      [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _i32, _vp]),
     ("inferop_w8a8_block_fp8_gemm_noalloc", ctypes.c_int,
      [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _i32, _vp]),
+    ("inferop_quant_w8a8_block_fp8_gemm", ctypes.c_int,
+     [_vp, _vp, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _i32, _vp]),
+    ("inferop_quant_w8a8_block_fp8_gemm_launches", ctypes.c_int, [_i64, _i64, _i64]),
     ("inferop_topk_softmax", ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp]),
     ("inferop_quant_fp8_weight_block", ctypes.c_int,
      [_vp, _vp, _vp, _i32, _i64, _i64, _i32, _i32, _vp]),

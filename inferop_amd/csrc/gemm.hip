@@ -51,6 +51,7 @@
 
 #include "device_common.h"
 #include "hip_launch.h"
+#include "quant_group.h"
 
 namespace inferop_hip {
 namespace {
@@ -744,6 +745,151 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
     if (p < kPairs && lane_row && row_of(q) < mend)
       store_out4<OUT_DT>(a, row_of(q), n0 + 16 * (p / MT) + 4 * c0, part[q]);
   }
+}
+
+// ---- decode GEMM that quantizes its own activations --------------------------------
+// quant_fp8_per_token_group (group 128) and the GEMM in one launch, for M <= 8.
+// grid: x = N stripes of 16 weight rows.  As the wide decode kernel with one
+// 8-row activation tile (AR = 8, NT = MT = 1, no K split): a workgroup owns
+// one stripe over the whole K range and its WK waves split the scale groups.
+// Each wave first issues its weight ring (UW groups, direct-to-LDS,
+// non-temporal), then quantizes the activation rows of all its groups with
+// the quantizer's own per-group code (qgroup::quant_group_lane: one DPP row
+// per (row, group), four per wave step, so the work is proportional to M)
+// into a private LDS region in the layout the MFMA operand read expects
+// (8 rows x 128 B per group, 16-byte chunks swizzled by row), with the
+// scales beside it.  Every (row, group) is also written to q / qs by exactly
+// one workgroup (the one whose index is the item's index modulo the grid), so
+// q and qs equal the quantizer's output.  The main loop streams the weights
+// through the ring in one fixed load pattern with one constant vmcnt wait and
+// multiplies in the same order as the 8-row wide decode kernel, whose output
+// it reproduces bit for bit.  Rows M..7 of the region are never written:
+// their MFMA columns are never stored.  The activations are quantized again
+// by every workgroup (M x K elements each), which only pays for a few rows;
+// the host sends larger M to the quantizer and the GEMM as two launches.
+__host__ __device__ constexpr int quant_gemm_cap() { return 8; }  // groups per wave
+
+template <int WK, int UW, int DT, int OUT_DT>
+__global__ __launch_bounds__(64 * WK) void gemm_quant_decode_kernel(GemmArgs a, const void* x,
+                                                                    uint8_t* q, float* qs) {
+  constexpr int kCap = quant_gemm_cap();
+  constexpr int kW = 2048;  // 16 weight rows x 128 B
+  constexpr int kA = 1024;  // 8 activation rows x 128 B
+  constexpr int kWave = UW * kW + kCap * kA + 8 * kCap * 4;
+  constexpr int kPerIter = 2;                  // loads issued per group
+  constexpr int kWait = (UW - 1) * kPerIter;   // loads that may stay in flight
+  static_assert(UW >= 2 && kWait <= 63, "ring size");
+  static_assert(WK * 64 * 16 <= WK * kWave, "the end-of-kernel sum fits in the slots");
+  using I = qgroup::In<DT>;
+  constexpr int kWords = I::kWords;           // 32-bit words of a lane's 8 elements
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[WK * kWave];
+
+  const int lane = threadIdx.x & 63;
+  const int wk = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int M = a.m, N = a.n, K = a.k;
+  const int KG = K >> 7;
+  const int NB = (N + 127) >> 7;
+  const int n0 = blockIdx.x * 16;
+  const int gw0 = wk * KG / WK, gw1 = (wk + 1) * KG / WK;
+  const int cnt = gw1 - gw0;
+  const int rsub = lane & 15, c0 = lane >> 4;
+  const int arow = rsub & 7;  // activation row a lane's MFMA column reads
+  const int lrow = lane >> 3;
+  const int loff = lrow * K + ((lane & 7) ^ lrow) * 16;
+  uint8_t* const wave_lds = smem + wk * kWave;
+  const uint32_t wbase = lds_addr(wave_lds);
+  uint8_t* const act = wave_lds + UW * kW;                          // [kCap][8][128]
+  float* const sa_l = reinterpret_cast<float*>(act + kCap * kA);   // [8][kCap]
+
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (cnt > 0) {
+    const u32x4 rB = rsrc_words(a.bq + (int64_t)n0 * K, (uint32_t)(min(16, N - n0) * K));
+    const float* sb_src = a.bs + (int64_t)min(n0 >> 7, NB - 1) * KG + gw0;
+    auto issue_w = [&](int i) {  // group gw0 + i into weight slot i % UW
+      const uint32_t dst = wbase + (uint32_t)(i % UW) * kW;
+      if (i >= cnt) {
+        // past the wave's last group: the same number of loads (of a weight
+        // scale), so the constant wait below stays exact
+#pragma unroll
+        for (int h = 0; h < 2; ++h) asm_global_to_lds4(sb_src, dst);
+        return;
+      }
+      const int g = gw0 + i;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        asm_buffer_to_lds16_nt(rB, dst + h * 1024, loff, 8 * h * K + g * 128);
+    };
+    for (int j = 0; j < UW; ++j) issue_w(j);
+
+    // Quantize the wave's (row, group) items while the weights stream in.
+    // The loads below are issued after the ring's, and memory operations
+    // complete in issue order, so their waits also cover the ring's first
+    // groups (which the first multiply needs anyway).
+    const float sbv = sb_src[min(lane, cnt - 1)];  // weight scale of group `lane`
+    const int sub = lane & 15;
+    const int items = M * cnt;
+    const int grid = (int)gridDim.x;
+    for (int t0 = 0; t0 < items; t0 += 4) {
+      const int tl = t0 + (lane >> 4);
+      const int t = min(tl, items - 1);  // every lane takes part in the row reduction
+      const int r = t / cnt, i = t - r * cnt, g = gw0 + i;
+      const int64_t e0 = (int64_t)r * K + g * 128 + sub * 8;  // first of the lane's 8 elements
+      uint32_t w[kWords];
+      const u32x4* src = reinterpret_cast<const u32x4*>(
+          reinterpret_cast<const uint8_t*>(x) + e0 * (DT == kFp32 ? 4 : 2));
+#pragma unroll
+      for (int v = 0; v < kWords / 4; ++v) {
+        const u32x4 tv = src[v];
+        w[4 * v + 0] = tv.x;
+        w[4 * v + 1] = tv.y;
+        w[4 * v + 2] = tv.z;
+        w[4 * v + 3] = tv.w;
+      }
+      uint32_t lo, hi;
+      float s;
+      qgroup::quant_group_lane<DT>(w, lo, hi, s);
+      if (tl < items) {
+        // bytes [8 sub, 8 sub + 8) of the row: half (sub & 1) of chunk sub / 2
+        *reinterpret_cast<u32x2*>(act + i * kA + r * 128 +
+                                  ((((sub >> 1) ^ (r & 7)) << 4) | ((sub & 1) << 3))) =
+            u32x2{lo, hi};
+        if (sub == 0) sa_l[r * kCap + i] = s;
+        if ((r * KG + g) % grid == (int)blockIdx.x) {
+          *reinterpret_cast<u32x2*>(q + e0) = u32x2{lo, hi};
+          if (sub == 0) qs[(int64_t)r * KG + g] = s;
+        }
+      }
+    }
+
+    for (int i = 0; i < cnt; ++i) {
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm(kWait));  // group i has landed
+      asm volatile("" ::: "memory");
+      const i32x8 wop = lds_operand(wave_lds + (i % UW) * kW, rsub, c0);
+      const f32x4 pv = mfma_group(wop, lds_operand(act + i * kA, arow, c0));
+      const float sb = __builtin_bit_cast(
+          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sbv), i));
+      const float sc = sa_l[arow * kCap + i] * sb;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] = __builtin_fmaf(pv[r], sc, acc[r]);
+      // the slot of group i is read (operand in registers) before refilling
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      issue_w(i + UW);
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm(0));  // tail loads have landed
+  }
+
+  // the WK waves' tiles summed through LDS in wave order (as the wide kernel)
+  if constexpr (WK > 1) {
+    __syncthreads();
+    f32x4* red = reinterpret_cast<f32x4*>(smem);  // [WK][64]
+    red[wk * 64 + lane] = acc;
+    __syncthreads();
+    if (wk != 0) return;
+    acc = red[lane];
+    for (int w = 1; w < WK; ++w) acc += red[w * 64 + lane];
+  }
+  if (rsub < 8 && rsub < M) store_out4<OUT_DT>(a, rsub, n0 + 4 * c0, acc);
 }
 
 // ---- prefill kernel --------------------------------------------------------------
@@ -2095,6 +2241,52 @@ extern "C" int inferop_hip_gemm_w8a8_block_noalloc(void* c, const uint8_t* a_q,
                                                    const inferop_gemm_launch* launch,
                                                    void* stream) {
   return gemm_block(c, a_q, a_scales, b_q, b_scales, m, n, k, out_dt, launch, stream, true);
+}
+
+namespace inferop_hip {
+namespace {
+template <int WK, int DT>
+using QuantGemmFn = void (*)(GemmArgs, const void*, uint8_t*, float*);
+template <int WK, int DT>
+constexpr QuantGemmFn<WK, DT> kQuantGemm[3] = {gemm_quant_decode_kernel<WK, 4, DT, kFp32>,
+                                               gemm_quant_decode_kernel<WK, 4, DT, kFp16>,
+                                               gemm_quant_decode_kernel<WK, 4, DT, kBf16>};
+template <int WK>
+void (*quant_gemm_fn(int32_t dt, int di))(GemmArgs, const void*, uint8_t*, float*) {
+  switch (dt) {
+    case kFp32: return kQuantGemm<WK, kFp32>[di];
+    case kFp16: return kQuantGemm<WK, kFp16>[di];
+    default: return kQuantGemm<WK, kBf16>[di];
+  }
+}
+}  // namespace
+}  // namespace inferop_hip
+
+extern "C" int inferop_hip_quant_gemm_decode(void* c, uint8_t* q, float* qs, const void* x,
+                                             int32_t dt, const uint8_t* b_q,
+                                             const float* b_scales, int64_t m, int64_t n,
+                                             int64_t k, int32_t out_dt, int32_t waves,
+                                             void* stream) {
+  const int di = dt_index(out_dt);
+  if (di < 0 || (dt != kFp32 && dt != kFp16 && dt != kBf16)) return hipErrorInvalidValue;
+  if (m < 1 || m > 8 || n <= 0 || k <= 0 || k % 128 != 0) return hipErrorInvalidValue;
+  if (n > 0x7FFFFFFF || 16 * k > 0x7FFFFFFF) return hipErrorInvalidValue;
+  if (waves != 4 && waves != 8) return hipErrorInvalidValue;
+  if ((k / 128 + waves - 1) / waves > quant_gemm_cap()) return hipErrorInvalidValue;
+  if ((uintptr_t)x % 16 != 0 || (uintptr_t)q % 8 != 0 || (uintptr_t)qs % 4 != 0)
+    return hipErrorInvalidValue;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int out_bytes = out_dt == kFp32 ? 4 : 2;
+  const int vec_ok = (n % 4 == 0) && ((uintptr_t)c % (size_t)(4 * out_bytes) == 0);
+  GemmArgs args{c,       nullptr, nullptr, b_q,    b_scales, nullptr,
+                nullptr, (int)m,  (int)n,  (int)k, vec_ok};
+  const unsigned grid = (unsigned)((n + 15) / 16);
+  if (waves == 8) {
+    hipLaunchKernelGGL(quant_gemm_fn<8>(dt, di), dim3(grid), dim3(512), 0, st, args, x, q, qs);
+  } else {
+    hipLaunchKernelGGL(quant_gemm_fn<4>(dt, di), dim3(grid), dim3(256), 0, st, args, x, q, qs);
+  }
+  return hipGetLastError();
 }
 
 extern "C" int inferop_hip_gemm_w8a8_block_grouped(void* c, const uint8_t* a_q,

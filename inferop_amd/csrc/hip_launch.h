@@ -104,6 +104,17 @@ int inferop_hip_gemm_w8a8_block_noalloc(void* c, const uint8_t* a_q, const float
                                         int64_t n, int64_t k, int32_t out_dt,
                                         const inferop_gemm_launch* launch, void* stream);
 
+/* The quantizer (group 128) fused with the decode GEMM, one launch: x [m, k]
+ * in dt (fp32 / fp16 / bf16, 16-byte aligned) is quantized exactly as
+ * inferop_hip_quant_fp8_group would (q [m, k] 8-byte aligned, qs [m, k/128])
+ * and C [m, n] = GEMM(q, qs, b_q, b_scales) exactly as the 8-row wide decode
+ * configuration with `waves` waves (4 or 8) computes it.  1 <= m <= 8 and at
+ * most 8 scale groups per wave (k / 128 <= 8 * waves); other calls return
+ * hipErrorInvalidValue without a launch. */
+int inferop_hip_quant_gemm_decode(void* c, uint8_t* q, float* qs, const void* x, int32_t dt,
+                                  const uint8_t* b_q, const float* b_scales, int64_t m, int64_t n,
+                                  int64_t k, int32_t out_dt, int32_t waves, void* stream);
+
 /* Grouped (MoE expert) GEMM; B [experts, n, k], b_scales [experts,
  * ceil(n/128), k/128]; C [m, n]; cfg must be a tiled configuration with a
  * grouped variant (inferop_gemm_cfg_info.grouped).

@@ -406,6 +406,16 @@ GemmChoice select_gemm(int64_t m, int64_t n, int64_t k, int cus) {
   const int64_t r128 = (t128 + 2 * cus - 1) / (2 * cus);
   if (2 * r256 * 3 < 2 * 2 * r128)
     return kg % 2 == 0 ? GemmChoice{kPerN256M256, tail_split()} : GemmChoice{kPreN256M256S2, 1};
+  // Fewer 256x256 tiles than CUs but at least as many 128x128 tiles (so the
+  // 128x128 tiles run unsplit, some CUs holding two), over a K of 48 scale
+  // groups or more: the persistent 256x256 tiles, all in their first, partial
+  // round and cut along K, read a quarter fewer operand bytes per CU
+  // (configs[4] M=1000, N=4672, K=7168: 76 tiles cut in 3, 68.2 -> 59.5 us;
+  // the 128x128 tiles put two on 40 CUs)
+  if (kg % 2 == 0 && kg >= 48 && t256 < cus && t128 >= cus) {
+    const int32_t s = tail_split();
+    if (s >= 2) return {kPerN256M256, s};
+  }
   // too few 128x128 tiles to fill the CUs: split K across workgroups, each
   // split keeping at least 16 scale groups (below that the fp32 partial
   // round trip costs more than the idle CUs) and at most four splits.
@@ -565,6 +575,39 @@ int gemm_impl(void* c, const void* a_q, const void* a_scales, const void* b_q,
   return gemm_launch(c, a_q, a_scales, b_q, b_scales, m, n, k, out_dt, ch.cfg, ch.split, stream);
 }
 
+// The quantizer and the GEMM in one call (the decode step's pair).  Where the
+// automatic GEMM choice is an unsplit 8-row wide decode configuration (M <= 8)
+// and every wave of it takes at most 8 scale groups, one kernel quantizes the
+// activations inside the GEMM; otherwise the quantizer and the GEMM run as two
+// launches on the stream.  Either way q / scales are the quantizer's output
+// and c the GEMM's with the automatic choice, bit for bit.
+int quant_gemm_plan(int64_t m, int64_t k, const GemmChoice& ch) {
+  if (m > 8 || ch.split != 1 || (ch.cfg != kDwM8K8 && ch.cfg != kDwM8K4)) return 0;
+  const int waves = ch.cfg == kDwM8K8 ? 8 : 4;
+  return (k / 128 + waves - 1) / waves <= 8 ? waves : 0;  // 8 groups per wave at most
+}
+
+int quant_gemm_impl(void* c, void* q, void* scales, const void* x, int32_t dt, const void* b_q,
+                    const void* b_scales, int64_t m, int64_t n, int64_t k, int32_t group_size,
+                    int32_t block_n, int32_t out_dt, void* stream) {
+  if (!gemm_shape_ok(m, n, k, group_size, block_n)) return INFEROP_ERR_SHAPE;
+  if (!valid_input_dtype(dt) || !valid_input_dtype(out_dt)) return INFEROP_ERR_DTYPE;
+  const DeviceEntry* d = gemm_device();
+  if (!d) return INFEROP_ERR_DEVICE;
+  const GemmChoice ch = choose_gemm_on(m, n, k, d->cus, stream);
+  const int waves = quant_gemm_plan(m, k, ch);
+  if (waves > 0 && aligned(x, 16) && aligned(q, 8) && aligned(scales, 4)) {
+    return status_of_hip(inferop_hip_quant_gemm_decode(
+        c, static_cast<uint8_t*>(q), static_cast<float*>(scales), x, dt,
+        static_cast<const uint8_t*>(b_q), static_cast<const float*>(b_scales), m, n, k, out_dt,
+        waves, stream));
+  }
+  const int st = status_of_hip(inferop_hip_quant_fp8_group(q, static_cast<float*>(scales), x, dt,
+                                                           m, k, 128, stream));
+  if (st != INFEROP_OK) return st;
+  return gemm_launch(c, q, scales, b_q, b_scales, m, n, k, out_dt, ch.cfg, ch.split, stream);
+}
+
 // Grouped (MoE expert) GEMM: the configuration from the mean rows per expert.
 // Up to 8 rows per expert (decode routings) the wide decode kernel: one
 // workgroup per (16-row weight stripe, expert tile) streams the stripe over
@@ -703,6 +746,14 @@ void w8a8_block_fp8_gemm(void* c, const void* a_q, const void* a_scales, const v
                   int32_t(out_dt), stream);
 }
 
+void quant_w8a8_block_fp8_gemm(void* c, void* q, void* scales, const void* x, dtype dt,
+                               const void* b_q, const void* b_scales, int64_t m, int64_t n,
+                               int64_t k, int group_size, int block_n, dtype out_dt,
+                               void* stream) {
+  (void)quant_gemm_impl(c, q, scales, x, int32_t(dt), b_q, b_scales, m, n, k, group_size, block_n,
+                        int32_t(out_dt), stream);
+}
+
 void w8a8_block_fp8_grouped_gemm(void* c, const void* a_q, const void* a_scales,
                                  const void* b_q, const void* b_scales,
                                  const void* expert_offsets, int64_t m, int64_t n, int64_t k,
@@ -783,6 +834,21 @@ extern "C" int inferop_w8a8_block_fp8_gemm(void* c, const void* a_q, const void*
                                            int64_t n, int64_t k, int32_t group_size,
                                            int32_t block_n, int32_t out_dt, void* stream) {
   return gemm_impl(c, a_q, a_scales, b_q, b_scales, m, n, k, group_size, block_n, out_dt, stream);
+}
+
+extern "C" int inferop_quant_w8a8_block_fp8_gemm(void* c, void* q, void* scales, const void* x,
+                                                 int32_t dt, const void* b_q, const void* b_scales,
+                                                 int64_t m, int64_t n, int64_t k,
+                                                 int32_t group_size, int32_t block_n,
+                                                 int32_t out_dt, void* stream) {
+  return quant_gemm_impl(c, q, scales, x, dt, b_q, b_scales, m, n, k, group_size, block_n, out_dt,
+                         stream);
+}
+
+extern "C" int inferop_quant_w8a8_block_fp8_gemm_launches(int64_t m, int64_t n, int64_t k) {
+  if (m <= 0 || n <= 0 || k <= 0 || k % 128 != 0) return -1;
+  const DeviceEntry* d = current_device();
+  return quant_gemm_plan(m, k, choose_gemm(m, n, k, d ? d->cus : 256)) > 0 ? 1 : 2;
 }
 
 extern "C" int inferop_w8a8_block_fp8_gemm_noalloc(void* c, const void* a_q, const void* a_scales,

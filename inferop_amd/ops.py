@@ -104,7 +104,22 @@ def w8a8_block_fp8_gemm(c, a_q, a_scales, b_q, b_scales, m: int, n: int, k: int,
         block_n, int(out_dt), _stream(stream))
 
 
-# ---- MoE routing (reference ops.h:102-110) ---------------------------------------
+def quant_w8a8_block_fp8_gemm(c, q, scales, x, dt, b_q, b_scales, m: int, n: int, k: int,
+                              group_size: int = 128, block_n: int = 128, out_dt=dtype.bf16,
+                              stream=None) -> int:
+    """quant_fp8_per_token_group then w8a8_block_fp8_gemm in one call (no
+    reference counterpart): the same q / scales / c, one launch up to 8 rows."""
+    return lib().inferop_quant_w8a8_block_fp8_gemm(
+        _ptr(c), _ptr(q), _ptr(scales), _ptr(x), int(dt), _ptr(b_q), _ptr(b_scales), m, n, k,
+        group_size, block_n, int(out_dt), _stream(stream))
+
+
+def quant_gemm_launches(m: int, n: int, k: int) -> int:
+    """Kernel launches quant_w8a8_block_fp8_gemm makes for this shape (1 or 2)."""
+    return lib().inferop_quant_w8a8_block_fp8_gemm_launches(m, n, k)
+
+
+# ---- allocation-free GEMM (no reference counterpart) -----------------------------
 def w8a8_block_fp8_gemm_noalloc(c, a_q, a_scales, b_q, b_scales, m: int, n: int, k: int,
                                 group_size: int = 128, block_n: int = 128, out_dt=dtype.bf16,
                                 stream=None) -> int:
@@ -116,6 +131,7 @@ def w8a8_block_fp8_gemm_noalloc(c, a_q, a_scales, b_q, b_scales, m: int, n: int,
         block_n, int(out_dt), _stream(stream))
 
 
+# ---- MoE routing (reference ops.h:102-110) ---------------------------------------
 def topk_softmax(topk_ids, topk_weights, logits, tokens: int, num_experts: int, topk: int,
                  renormalize: bool = True, stream=None) -> int:
     return lib().inferop_topk_softmax(_ptr(topk_ids), _ptr(topk_weights), _ptr(logits), tokens,

@@ -128,6 +128,16 @@ int inferop_hip_gemm_w8a8_block_noalloc(void*, const uint8_t*, const float*, con
                                         const inferop_gemm_launch* l, void*) {
   return gemm_stub(l, m, n, k, dt);
 }
+int g_fused_launches = 0;
+int inferop_hip_quant_gemm_decode(void*, uint8_t*, float*, const void*, int32_t dt, const uint8_t*,
+                                  const float*, int64_t m, int64_t n, int64_t k, int32_t out_dt,
+                                  int32_t waves, void*) {
+  check(dt >= 0 && dt <= 2 && out_dt >= 0 && out_dt <= 2, "fused dtypes");
+  check(m >= 1 && m <= 8 && n > 0 && k % 128 == 0, "fused shape");
+  check((waves == 4 || waves == 8) && (k / 128 + waves - 1) / waves <= 8, "fused waves");
+  ++g_fused_launches;
+  return 0;
+}
 int inferop_hip_gemm_w8a8_block_grouped(void*, const uint8_t*, const float*, const uint8_t*,
                                         const float*, const int32_t*, int64_t m, int64_t n,
                                         int64_t k, int64_t experts, int64_t max_m, int32_t,
@@ -198,6 +208,20 @@ void host_layer() {
               "masked select");
       }
   check(launches > 1000, "selection sweep ran");
+  // the quantizer fused with the GEMM: one launch exactly where the plan says
+  for (int64_t m : ms)
+    for (int64_t n : ns)
+      for (int64_t k : ks) {
+        if (m * n > (int64_t(1) << 34) || m * k > (int64_t(1) << 34)) continue;
+        alignas(16) int8_t buf[64] = {};
+        const int before = g_fused_launches;
+        check(inferop_quant_w8a8_block_fp8_gemm(buf, buf, buf, buf, 2, buf, buf, m, n, k, 128, 128,
+                                                2, nullptr) == INFEROP_OK,
+              "fused call");
+        check((g_fused_launches - before == 1) ==
+                  (inferop_quant_w8a8_block_fp8_gemm_launches(m, n, k) == 1),
+              "fused launch count");
+      }
   // rejected shapes and dtypes, including values that would overflow a product
   int8_t d[16] = {};
   check(inferop_w8a8_block_fp8_gemm(d, d, d, d, d, 4, 8, 100, 128, 128, 2, nullptr) ==

@@ -250,6 +250,10 @@ def test_gemm_selection_covers_configs():
     # up to 256 rows with many 128x128 tiles and a long K: persistent 256x256
     assert sel(160, 18432, 7168) == ("per_n256_m256_w8", 3)
     assert sel(160, 24576, 1536) == ("pre_n128_m128_w4_s2", 1)
+    # fewer 256x256 tiles than CUs, at least as many 128x128 tiles, a long K:
+    # persistent 256x256 tiles cut along K (configs[4] M=1000)
+    assert sel(1000, 4672, 7168) == ("per_n256_m256_w8", 3)
+    assert sel(1024, 7168, 2048) == ("pre_n128_m128_w4_s2", 1)
     # 256x256 prefill tiles run on the persistent kernel when K / 128 is even,
     # on the one-tile-per-workgroup kernel otherwise
     assert names[inferop_amd.gemm_select(4096, 7168, 16384)[0]] == "per_n256_m256_w8"
