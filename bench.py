@@ -127,6 +127,23 @@ def traffic_pass():
         cfg, split = ia.gemm_select(m, n, k)
         launches.append({"launch": f"gemm m={m} n={n} k={k} {ia.gemm_config_name(cfg)}/s{split}",
                          "read": gemm_bytes(m, n, k) - 2 * m * n, "write": 2 * m * n})
+    # the quantizer fused with the GEMM, where it is one launch (M <= 8), on
+    # weight copies no earlier launch touched
+    for (m, n, k), a in zip(cases, acts):
+        if ia.quant_gemm_launches(m, n, k) != 1:
+            continue
+        bq = torch.randint(0, 0x7E, (n, k), generator=gen, device=dev,
+                           dtype=torch.int32).to(torch.uint8)
+        bs = torch.rand(((n + 127) // 128, k // 128), generator=gen, device=dev) * 1e-3 + 1e-4
+        q = torch.empty((m, k), dtype=torch.uint8, device=dev)
+        s = torch.empty((m, k // 128), dtype=torch.float32, device=dev)
+        c = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+        torch.cuda.synchronize()
+        assert ia.quant_w8a8_block_fp8_gemm(c, q, s, a, ia.dtype.bf16, bq, bs, m, n, k) == 0
+        torch.cuda.synchronize()
+        launches.append({"launch": f"quant+gemm m={m} n={n} k={k} (one launch)",
+                         "read": 2 * m * k + n * k + 4 * ((n + 127) // 128) * (k // 128),
+                         "write": m * k + 4 * m * (k // 128) + 2 * m * n})
     print(json.dumps({"traffic_pass": launches}), flush=True)
 
 

@@ -753,35 +753,38 @@ __global__ __launch_bounds__(64 * WK) void gemm_decode_wide_kernel(GemmArgs a) {
 // 8-row activation tile (AR = 8, NT = MT = 1, no K split): a workgroup owns
 // one stripe over the whole K range and its WK waves split the scale groups.
 // Each wave first issues its weight ring (UW groups, direct-to-LDS,
-// non-temporal), then quantizes the activation rows of all its groups with
-// the quantizer's own per-group code (qgroup::quant_group_lane: one DPP row
-// per (row, group), four per wave step, so the work is proportional to M)
+// non-temporal), then the loads of the activation rows of all its groups at
+// once (so they cost one round trip, not one per group), then quantizes them
+// with the quantizer's own per-group code (qgroup::quant_group_lane: one DPP
+// row per (row, group), four per step, so the work is proportional to M)
 // into a private LDS region in the layout the MFMA operand read expects
 // (8 rows x 128 B per group, 16-byte chunks swizzled by row), with the
 // scales beside it.  Every (row, group) is also written to q / qs by exactly
 // one workgroup (the one whose index is the item's index modulo the grid), so
-// q and qs equal the quantizer's output.  The main loop streams the weights
-// through the ring in one fixed load pattern with one constant vmcnt wait and
-// multiplies in the same order as the 8-row wide decode kernel, whose output
-// it reproduces bit for bit.  Rows M..7 of the region are never written:
-// their MFMA columns are never stored.  The activations are quantized again
-// by every workgroup (M x K elements each), which only pays for a few rows;
-// the host sends larger M to the quantizer and the GEMM as two launches.
+// q and qs equal the quantizer's output.  The main loop then streams the
+// weights through the ring as the wide decode kernel does (one fixed load
+// pattern, one constant vmcnt wait) and multiplies in the same order as the
+// 8-row wide decode kernel, whose output it reproduces bit for bit.  Rows
+// M..7 of the region are never written: their MFMA columns are never stored.
+// The activations are quantized again by every workgroup (M x K elements
+// each), which only pays for a few rows; the host sends larger M to the
+// quantizer and the GEMM as two launches.
 __host__ __device__ constexpr int quant_gemm_cap() { return 8; }  // groups per wave
 
-template <int WK, int UW, int DT, int OUT_DT>
+template <int WK, int DT, int OUT_DT>
 __global__ __launch_bounds__(64 * WK) void gemm_quant_decode_kernel(GemmArgs a, const void* x,
                                                                     uint8_t* q, float* qs) {
+  constexpr int UW = 4;
   constexpr int kCap = quant_gemm_cap();
-  constexpr int kW = 2048;  // 16 weight rows x 128 B
-  constexpr int kA = 1024;  // 8 activation rows x 128 B
+  constexpr int kSteps = 8 * kCap / 4;  // (row, group) items, four per step
+  constexpr int kW = 2048;              // 16 weight rows x 128 B
+  constexpr int kA = 1024;              // 8 activation rows x 128 B
   constexpr int kWave = UW * kW + kCap * kA + 8 * kCap * 4;
-  constexpr int kPerIter = 2;                  // loads issued per group
-  constexpr int kWait = (UW - 1) * kPerIter;   // loads that may stay in flight
-  static_assert(UW >= 2 && kWait <= 63, "ring size");
+  constexpr int kPerIter = 2;                // loads issued per group
+  constexpr int kWait = (UW - 1) * kPerIter;  // loads that may stay in flight
   static_assert(WK * 64 * 16 <= WK * kWave, "the end-of-kernel sum fits in the slots");
   using I = qgroup::In<DT>;
-  constexpr int kWords = I::kWords;           // 32-bit words of a lane's 8 elements
+  constexpr int kWords = I::kWords;  // 32-bit words of a lane's 8 elements
   __shared__ __attribute__((aligned(1024))) uint8_t smem[WK * kWave];
 
   const int lane = threadIdx.x & 63;
@@ -798,8 +801,8 @@ __global__ __launch_bounds__(64 * WK) void gemm_quant_decode_kernel(GemmArgs a, 
   const int loff = lrow * K + ((lane & 7) ^ lrow) * 16;
   uint8_t* const wave_lds = smem + wk * kWave;
   const uint32_t wbase = lds_addr(wave_lds);
-  uint8_t* const act = wave_lds + UW * kW;                          // [kCap][8][128]
-  float* const sa_l = reinterpret_cast<float*>(act + kCap * kA);   // [8][kCap]
+  uint8_t* const act = wave_lds + UW * kW;                        // [kCap][8][128]
+  float* const sa_l = reinterpret_cast<float*>(act + kCap * kA);  // [8][kCap]
 
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
   if (cnt > 0) {
@@ -819,44 +822,57 @@ __global__ __launch_bounds__(64 * WK) void gemm_quant_decode_kernel(GemmArgs a, 
       for (int h = 0; h < 2; ++h)
         asm_buffer_to_lds16_nt(rB, dst + h * 1024, loff, 8 * h * K + g * 128);
     };
+#pragma unroll
     for (int j = 0; j < UW; ++j) issue_w(j);
 
-    // Quantize the wave's (row, group) items while the weights stream in.
-    // The loads below are issued after the ring's, and memory operations
-    // complete in issue order, so their waits also cover the ring's first
-    // groups (which the first multiply needs anyway).
+    // The wave's (row, group) items, four per step: every load first (the
+    // steps are unrolled and predicated, so the values stay in registers and
+    // the loads travel together), then the quantization.  Memory operations
+    // complete in issue order, so the wait for these loads also covers the
+    // ring's first groups, which the first multiply needs anyway.
     const float sbv = sb_src[min(lane, cnt - 1)];  // weight scale of group `lane`
     const int sub = lane & 15;
     const int items = M * cnt;
-    const int grid = (int)gridDim.x;
-    for (int t0 = 0; t0 < items; t0 += 4) {
-      const int tl = t0 + (lane >> 4);
-      const int t = min(tl, items - 1);  // every lane takes part in the row reduction
-      const int r = t / cnt, i = t - r * cnt, g = gw0 + i;
-      const int64_t e0 = (int64_t)r * K + g * 128 + sub * 8;  // first of the lane's 8 elements
-      uint32_t w[kWords];
-      const u32x4* src = reinterpret_cast<const u32x4*>(
-          reinterpret_cast<const uint8_t*>(x) + e0 * (DT == kFp32 ? 4 : 2));
+    const int steps = (items + 3) >> 2;
+    uint32_t w[kSteps][kWords];
 #pragma unroll
-      for (int v = 0; v < kWords / 4; ++v) {
-        const u32x4 tv = src[v];
-        w[4 * v + 0] = tv.x;
-        w[4 * v + 1] = tv.y;
-        w[4 * v + 2] = tv.z;
-        w[4 * v + 3] = tv.w;
+    for (int st = 0; st < kSteps; ++st) {
+      if (st < steps) {
+        const int t = min(4 * st + (lane >> 4), items - 1);
+        const int r = t / cnt, i = t - r * cnt;
+        const int64_t e0 = (int64_t)r * K + (gw0 + i) * 128 + sub * 8;
+        const u32x4* src = reinterpret_cast<const u32x4*>(
+            reinterpret_cast<const uint8_t*>(x) + e0 * (DT == kFp32 ? 4 : 2));
+#pragma unroll
+        for (int v = 0; v < kWords / 4; ++v) {
+          const u32x4 tv = src[v];
+          w[st][4 * v + 0] = tv.x;
+          w[st][4 * v + 1] = tv.y;
+          w[st][4 * v + 2] = tv.z;
+          w[st][4 * v + 3] = tv.w;
+        }
       }
-      uint32_t lo, hi;
-      float s;
-      qgroup::quant_group_lane<DT>(w, lo, hi, s);
-      if (tl < items) {
-        // bytes [8 sub, 8 sub + 8) of the row: half (sub & 1) of chunk sub / 2
-        *reinterpret_cast<u32x2*>(act + i * kA + r * 128 +
-                                  ((((sub >> 1) ^ (r & 7)) << 4) | ((sub & 1) << 3))) =
-            u32x2{lo, hi};
-        if (sub == 0) sa_l[r * kCap + i] = s;
-        if ((r * KG + g) % grid == (int)blockIdx.x) {
-          *reinterpret_cast<u32x2*>(q + e0) = u32x2{lo, hi};
-          if (sub == 0) qs[(int64_t)r * KG + g] = s;
+    }
+    const int grid = (int)gridDim.x;
+#pragma unroll
+    for (int st = 0; st < kSteps; ++st) {
+      if (st < steps) {
+        const int tl = 4 * st + (lane >> 4);
+        const int t = min(tl, items - 1);  // every lane takes part in the row reduction
+        const int r = t / cnt, i = t - r * cnt, g = gw0 + i;
+        uint32_t lo, hi;
+        float s;
+        qgroup::quant_group_lane<DT>(w[st], lo, hi, s);
+        if (tl < items) {
+          // bytes [8 sub, 8 sub + 8) of the row: half (sub & 1) of chunk sub / 2
+          *reinterpret_cast<u32x2*>(act + i * kA + r * 128 +
+                                    ((((sub >> 1) ^ (r & 7)) << 4) | ((sub & 1) << 3))) =
+              u32x2{lo, hi};
+          if (sub == 0) sa_l[r * kCap + i] = s;
+          if ((r * KG + g) % grid == (int)blockIdx.x) {
+            *reinterpret_cast<u32x2*>(q + (int64_t)r * K + g * 128 + sub * 8) = u32x2{lo, hi};
+            if (sub == 0) qs[(int64_t)r * KG + g] = s;
+          }
         }
       }
     }
@@ -2248,9 +2264,9 @@ namespace {
 template <int WK, int DT>
 using QuantGemmFn = void (*)(GemmArgs, const void*, uint8_t*, float*);
 template <int WK, int DT>
-constexpr QuantGemmFn<WK, DT> kQuantGemm[3] = {gemm_quant_decode_kernel<WK, 4, DT, kFp32>,
-                                               gemm_quant_decode_kernel<WK, 4, DT, kFp16>,
-                                               gemm_quant_decode_kernel<WK, 4, DT, kBf16>};
+constexpr QuantGemmFn<WK, DT> kQuantGemm[3] = {gemm_quant_decode_kernel<WK, DT, kFp32>,
+                                               gemm_quant_decode_kernel<WK, DT, kFp16>,
+                                               gemm_quant_decode_kernel<WK, DT, kBf16>};
 template <int WK>
 void (*quant_gemm_fn(int32_t dt, int di))(GemmArgs, const void*, uint8_t*, float*) {
   switch (dt) {
