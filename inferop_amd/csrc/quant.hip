@@ -138,7 +138,8 @@ __global__ __launch_bounds__(256) void quant_generic_kernel(uint8_t* __restrict_
 // 16-bit outputs, two for fp32 (4096x7168: bf16 20.9 -> 18.5 us, fp32 44.6 ->
 // 31.5 us against 16 elements per lane, whose per-lane 32 / 64 output bytes
 // left each store instruction a quarter or half of every cache line).
-template <int DT>
+// NTS: non-temporal stores of 16-bit outputs (see launch_dequant)
+template <int DT, bool NTS = false>
 __global__ __launch_bounds__(256) void dequant_v8_kernel(void* __restrict__ x,
                                                          const uint8_t* __restrict__ q,
                                                          const float* __restrict__ scales,
@@ -167,7 +168,11 @@ __global__ __launch_bounds__(256) void dequant_v8_kernel(void* __restrict__ x,
     u32x4 buf;  // the 8 outputs, converted as store4 converts them
     store4<DT>(reinterpret_cast<T*>(&buf), v[0], v[1], v[2], v[3]);
     store4<DT>(reinterpret_cast<T*>(&buf) + 4, v[4], v[5], v[6], v[7]);
-    *reinterpret_cast<u32x4*>(dst) = buf;
+    if (NTS) {
+      __builtin_nontemporal_store(buf, reinterpret_cast<u32x4*>(dst));
+    } else {
+      *reinterpret_cast<u32x4*>(dst) = buf;
+    }
   }
 }
 
@@ -234,8 +239,16 @@ hipError_t launch_dequant(void* x, const uint8_t* q, const float* scales, int64_
     const int64_t nvec = total / 8;
     const int64_t blocks = (nvec + 255) / 256;
     if (blocks > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL((dequant_v8_kernel<DT>), dim3((unsigned)blocks), dim3(256), 0, st, x, q,
-                       scales, nvec, gs);
+    // 16-bit outputs: non-temporal stores outside 64..256 MiB of codes and
+    // outputs (bf16, A/B on one box: 8192x18432 77.2 -> 72.2 us, 1024x7168
+    // 5.7 -> 5.1 us); inside that band, where codes and outputs fit the
+    // Infinity Cache, cached stores (8192x7168: 29.5 against 30.2 us).  fp32
+    // outputs keep cached stores: a lane's two 16-byte stores cover half
+    // lines each, and non-temporal ones took 4096x7168 from 28.5 to 38 us.
+    const int64_t bytes = total * (int64_t)(1 + sizeof(typename OutT<DT>::T));
+    const bool nts = DT != kFp32 && (bytes < (int64_t)64 << 20 || bytes > (int64_t)256 << 20);
+    auto fn = nts ? dequant_v8_kernel<DT, true> : dequant_v8_kernel<DT, false>;
+    hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(256), 0, st, x, q, scales, nvec, gs);
   } else {
     const int64_t blocks = (total + 255) / 256;
     if (blocks > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
