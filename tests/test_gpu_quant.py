@@ -130,6 +130,14 @@ def test_quant_large_whole_tensor_and_roundtrip():
     sg = s.repeat_interleave(128, dim=1)
     tol = torch.maximum(xf.abs() / 16, sg * 1.5e-3)
     assert bool(((xd - xf).abs() <= tol).all())
+    # 16-bit outputs at this size (201 MB of codes and outputs: the
+    # cached-store band of the dequantizer) are the fp32 products rounded to
+    # the output type
+    for odt, code in ((torch.bfloat16, DT.bf16), (torch.float16, DT.fp16)):
+        xh = torch.empty((m, k), dtype=odt, device="cuda:0")
+        assert inferop_amd.dequant_fp8_per_token_group(xh, code, q, s, m, k) == 0
+        assert torch.equal(xh.view(torch.int16), xd.to(odt).view(torch.int16)), str(odt)
+        del xh
 
 
 @pytest.mark.gpu
