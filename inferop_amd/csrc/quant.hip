@@ -208,15 +208,17 @@ hipError_t launch_quant(void* q, float* scales, const void* x, int64_t rows, int
       if (blocks > 0x7FFFFFFF) return hipErrorInvalidConfiguration;
       // Cached loads and stores while input and codes together fit the
       // 256 MiB Infinity Cache (4096x7168 bf16: 16.3 -> 16.0 us, 4096x16384:
-      // 33.9 -> 33.3 us); beyond it non-temporal loads, which keep the input
-      // stream from evicting the codes, with cached stores (8192x18432:
-      // 71.9 -> 69.5 us; cached loads there 79.6 us).  Below 64 MiB both
-      // stay non-temporal (1024x7168 with cached ones: 5.8 -> 6.7 us).
+      // 33.9 -> 33.3 us; fp32 4096x7168 28.1 -> 26.3 us); beyond it
+      // non-temporal loads, which keep the input stream from evicting the
+      // codes, with cached stores for 16-bit inputs (8192x18432 bf16: 71.9 ->
+      // 69.5 us; cached loads there 79.6 us) and non-temporal ones for fp32
+      // (cached: 130.5 -> 134.4 us).  Below 64 MiB both stay non-temporal
+      // (1024x7168 bf16 with cached ones: 5.8 -> 6.7 us).
       // input bytes per element (kWords words carry 8 elements) plus the code
       const int64_t bytes = rows * cols * (int64_t)(In<DT>::kWords / 2 + 1);
       auto fn = bytes < (int64_t)64 << 20     ? quant_g128_kernel<DT, U, true, true>
                 : bytes <= (int64_t)256 << 20 ? quant_g128_kernel<DT, U, false, false>
-                                              : quant_g128_kernel<DT, U, true, false>;
+                                              : quant_g128_kernel<DT, U, true, DT == kFp32>;
       hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(256), 0, st, (uint8_t*)q, scales,
                          (const uint32_t*)x, ngroups);
     }
