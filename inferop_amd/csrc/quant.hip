@@ -512,49 +512,27 @@ __device__ __forceinline__ float silu_of(float g) {
 }
 __device__ __forceinline__ float silu_mul(float g, float u) { return silu_of(g) * u; }
 
-// For bf16 gates, g / (1 + exp(-g)) depends only on the gate's 16 bits: a
+// For 16-bit gates, g / (1 + exp(-g)) depends only on the gate's 16 bits: a
 // table of the fp32 value for each of the 65536 patterns (built on the device
 // by silu_of, so the entries are bit for bit what the arithmetic above
 // gives), indexed by the bits, leaves one gather and the reference's final
-// multiply per element (4096x18432: 146 -> 111 us on one box).  The gates of
-// a layer touch a few thousand entries, which stay in the L1 cache.  fp16
-// gates, with 10-bit mantissas, spread over about 8 times as many entries and
-// gathers from a full fp16 table cost more than the arithmetic (181 us against
-// about 146 us); small fp16 calls compute, large ones use the exponential
-// pair below from LDS.  One set of tables per GPU (static device memory, held
-// until the process ends), built by silu_table_build_kernel at the first bf16
-// or fp16 call on the device (see launch_silu_mul_quant); a launch that finds
-// no table evaluates the arithmetic instead, and both give the same bits.
+// multiply per element (bf16 4096x18432: 146 -> 111 us on one box).  The bf16
+// gates of a layer touch a few thousand entries, which stay in the L1 cache;
+// fp16 gates, with 10-bit mantissas, spread over about 8 times as many, and
+// gathers from the full fp16 table cost more than the arithmetic (181 us
+// against about 146 us), so large calls gather from a slice of each table
+// held in LDS (below).  One set of tables per GPU (static device memory,
+// held until the process ends), built by silu_table_build_kernel at the
+// first bf16 or fp16 call on the device (see launch_silu_mul_quant); a
+// launch that finds no table evaluates the arithmetic instead, and both give
+// the same bits.
 __device__ float silu_table_bf16[65536];
-
-// For fp16 gates exp(-g) = exp(-g_hi) * exp(-g_lo) in double, where g_hi
-// is g with its low 7 mantissa bits cleared and g_lo = g - g_hi (exact):
-// 512 + 8192 doubles indexed by (sign, exponent field, top 3 / low 7 mantissa
-// bits), filled with the device's double exponential.  The product carries
-// the same few double ulps of error as one exp call, so rounding it to fp32
-// gives the value silu_of uses except within ~2^-50 relative of an fp32
-// rounding midpoint.
-__device__ double silu_exp_hi_f16[512];
-__device__ double silu_exp_lo_f16[8192];
-
-// fp16 value of (sign, exponent field, mantissa) in double (exact).
-__device__ __forceinline__ double f16_parts(uint32_t s, uint32_t e, uint32_t m) {
-  const double mag = e == 0 ? ldexp((double)m, -24) : ldexp((double)(1024 + m), (int)e - 25);
-  return s ? -mag : mag;
-}
+__device__ float silu_table_f16[65536];
 
 __global__ __launch_bounds__(256) void silu_table_build_kernel() {
   const uint32_t b = blockIdx.x * 256 + threadIdx.x;
   silu_table_bf16[b] = silu_of(u2f(b << 16));
-  if (b < 8192) {  // (sign, exponent, low 7 bits): exp(-g_lo)
-    const uint32_t s = b >> 12, e = (b >> 7) & 31, ml = b & 127;
-    const double gl = f16_parts(s, e, ml) - f16_parts(s, e, 0);
-    silu_exp_lo_f16[b] = ::exp(-gl);
-  }
-  if (b < 512) {  // (sign, exponent, top 3 bits): exp(-g_hi)
-    const uint32_t s = b >> 8, e = (b >> 3) & 31, mh = b & 7;
-    silu_exp_hi_f16[b] = ::exp(-f16_parts(s, e, mh << 7));
-  }
+  silu_table_f16[b] = silu_of((float)__builtin_bit_cast(_Float16, (uint16_t)b));
 }
 
 // Most of the table is one of three exact rules.  For a bf16 gate g with
@@ -596,17 +574,44 @@ __device__ __forceinline__ float silu_bf16_lds(const float* tab, uint32_t gbits)
   return rel < 32u ? t : rule;
 }
 
-// fp16 gate g (exactly representable) -> silu(g) from the two LDS tables
-// (tlo: 8192 doubles, thi: 512); Inf / NaN gates are left to the caller.
-__device__ __forceinline__ float silu_f16_lds(const double* tlo, const double* thi, float g) {
+// fp16 gates: the slice of silu_table_f16 for exponent fields [11, 17)
+// (2^-4 <= |g| < 4) of both signs, 2 x 6 x 1024 entries, 48 KB (three
+// workgroups per CU), holds all but about 5% of normally distributed gates;
+// the rest (and Inf / NaN) gather from the full table.  LDS entry
+// i = sign * 6144 + (E - 11) * 1024 + mantissa.  Measured on 4096x18432
+// (graph over > 1 GiB of inputs): the double exponential pair this replaced
+// 119-122 us; slices of 8 exponents (64 KB, two workgroups per CU) 96 us,
+// 6 exponents 92 us, 5 (four per CU) 93-96 us, 4 exponents 113 us.
+constexpr uint32_t kSiluF16LoExp = 11;
+constexpr int kSiluF16Exps = 6;
+constexpr int kSiluF16LdsEntries = 2 * kSiluF16Exps * 1024;
+
+template <int NT>
+__device__ __forceinline__ void silu_f16_lds_fill(float* tab) {
+  static_assert(kSiluF16LdsEntries % (4 * NT) == 0, "whole 16-byte chunks per thread");
+  const u32x4* src = reinterpret_cast<const u32x4*>(silu_table_f16);
+  u32x4* dst = reinterpret_cast<u32x4*>(tab);
+#pragma unroll
+  for (int j = 0; j < kSiluF16LdsEntries / 4 / NT; ++j) {
+    const int v = j * NT + (int)threadIdx.x;  // 16-byte chunk of the slice
+    const uint32_t i = (uint32_t)v * 4;
+    const uint32_t sign = i / (kSiluF16Exps * 1024), e = kSiluF16LoExp + (i >> 10) % kSiluF16Exps;
+    dst[v] = src[((sign << 15) | (e << 10) | (i & 1023u)) / 4];
+  }
+}
+
+// silu(g) for the fp16 gate g (exactly representable in fp16).
+__device__ __forceinline__ float silu_f16_lds(const float* tab, float g) {
   const uint32_t b = __builtin_bit_cast(uint16_t, (_Float16)g);
-  const double p = thi[b >> 7] * tlo[((b & 0xFC00u) >> 3) | (b & 127u)];
-  return g / (1.0f + (float)p);
+  const uint32_t rel = ((b >> 10) & 31u) - kSiluF16LoExp;  // wraps below the slice
+  return rel < (uint32_t)kSiluF16Exps
+             ? tab[(b >> 15) * (kSiluF16Exps * 1024) + (rel << 10) + (b & 1023u)]
+             : silu_table_f16[b];
 }
 
 // gate_up: [tokens, 2d] dt (bf16 or fp16) -> q [tokens, d] E4M3, scales
-// [tokens, d/128], with the tables in LDS (bf16: the 32 KB SiLU slice; fp16:
-// the 68 KB exponential pair).  Lane layout as silu_mul_quant_kernel (16
+// [tokens, d/128], with a slice of the SiLU table in LDS (bf16: 32 KB; fp16:
+// 48 KB).  Lane layout as silu_mul_quant_kernel (16
 // lanes per 128-output group, 4 groups per wave and step, U steps issued
 // together); NT-thread workgroups stride over the groups so each copies the
 // tables once, and large workgroups let more waves share one copy.
@@ -617,18 +622,13 @@ __global__ __launch_bounds__(NT) void silu_mul_quant_lds_kernel(uint8_t* __restr
                                                                  uint32_t d, uint32_t gpr,
                                                                  uint32_t ngroups) {
   static_assert(DT == kBf16 || DT == kFp16, "16-bit gates only");
-  constexpr int kBytes = DT == kBf16 ? kSiluLdsEntries * 4 : (8192 + 512) * 8;
+  constexpr int kBytes = (DT == kBf16 ? kSiluLdsEntries : kSiluF16LdsEntries) * 4;
   __shared__ __align__(16) uint8_t lds[kBytes];
   float* tab = reinterpret_cast<float*>(lds);
-  double* tlo = reinterpret_cast<double*>(lds);
-  double* thi = tlo + 8192;
   if constexpr (DT == kBf16) {
     silu_lds_fill<NT>(tab);
   } else {
-    const u32x4* lo = reinterpret_cast<const u32x4*>(silu_exp_lo_f16);
-    const u32x4* hi = reinterpret_cast<const u32x4*>(silu_exp_hi_f16);
-    u32x4* dst = reinterpret_cast<u32x4*>(lds);
-    for (int v = threadIdx.x; v < 4096 + 256; v += NT) dst[v] = v < 4096 ? lo[v] : hi[v - 4096];
+    silu_f16_lds_fill<NT>(tab);
   }
   __syncthreads();
   const int lane = threadIdx.x & 63;
@@ -657,8 +657,8 @@ __global__ __launch_bounds__(NT) void silu_mul_quant_lds_kernel(uint8_t* __restr
     for (int u = 0; u < U; ++u) {
       const uint32_t g = (uint32_t)base + 4 * u + (lane >> 4);
       float y[8];
-      bool special = false;
       if constexpr (DT == kBf16) {
+        bool special = false;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           y[i] = silu_bf16_lds(tab, f2u(gv[u][i]));
@@ -671,15 +671,7 @@ __global__ __launch_bounds__(NT) void silu_mul_quant_lds_kernel(uint8_t* __restr
         }
       } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          y[i] = silu_f16_lds(tlo, thi, gv[u][i]);
-          special |= (f2u(gv[u][i]) & 0x7F800000u) == 0x7F800000u;
-        }
-        if (special) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i)
-            if ((f2u(gv[u][i]) & 0x7F800000u) == 0x7F800000u) y[i] = silu_of(gv[u][i]);
-        }
+        for (int i = 0; i < 8; ++i) y[i] = silu_f16_lds(tab, gv[u][i]);
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i) y[i] *= uv[u][i];
@@ -919,8 +911,8 @@ hipError_t launch_silu_mul_quant(uint8_t* q, float* scales, const void* gate_up,
   const int64_t ngroups = tokens * (d / 128);
   if constexpr (DT == kFp16) {
     if (silu_table(st)) {
-      // 68 KB of LDS per workgroup: two 512-thread workgroups per CU
-      constexpr int UL = 2, NT = 512, kWgPerCu = 2;
+      // 48 KB of LDS per workgroup: three 512-thread workgroups per CU
+      constexpr int UL = 2, NT = 512, kWgPerCu = 3;
       constexpr int kStep = NT / 16 * UL;
       int cus = 0;
       if (hipError_t e = silu_device_cus(&cus); e != hipSuccess) return e;

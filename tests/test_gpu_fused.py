@@ -89,12 +89,12 @@ def test_silu_quant_every_gate_value(kind):
 @pytest.mark.parametrize("kind", ["bf16", "fp16"])
 def test_silu_lds_tables_match_small_call_kernel(kind):
     # 32768 tokens x 128 outputs = 32768 groups take the kernel that holds
-    # its SiLU tables in LDS (it needs 64 groups per CU: 16384 on 256 CUs);
-    # 512-token calls take the kernel that gathers from the full bf16 table
-    # or evaluates the double exponential for fp16.  Rows are independent, so
-    # both must give the same bits for every 16-bit gate pattern, Inf and NaN
-    # included (fp16: exp(-g_hi) * exp(-g_lo) in double rounds to the same
-    # fp32 as one exp call for every pattern).
+    # a slice of its SiLU table in LDS (it needs 64 groups per CU: 16384 on
+    # 256 CUs) and gathers the other patterns from the full table; 512-token
+    # calls take the kernel that gathers from the full bf16 table or
+    # evaluates the SiLU for fp16.  Rows are independent, so both must give
+    # the same bits for every 16-bit gate pattern, Inf and NaN included (the
+    # tables hold the same arithmetic's results).
     device()
     tokens, d = 32768, 128
     pats = np.arange(65536, dtype=np.uint32).astype(np.uint16)
