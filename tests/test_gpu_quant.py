@@ -141,6 +141,26 @@ def test_quant_large_whole_tensor_and_roundtrip():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("kind,m,k", [("fp16", 4096, 7168), ("fp16", 8192, 18432),
+                                      ("fp32", 2048, 7168), ("fp32", 8192, 18432)])
+def test_quant_cache_policy_sizes_whole_tensor(kind, m, k):
+    # the quantizer's cached-access band (64-256 MiB of input and codes) and
+    # the sizes above it, for fp16 and fp32 inputs: every byte and scale
+    # against the oracle
+    device()
+    print(f"quant {kind} {m}x{k}", flush=True)
+    g = torch.Generator(device="cuda:0").manual_seed(m + k)
+    x = torch.randn((m, k), generator=g, device="cuda:0")
+    if kind == "fp16":
+        x = x.half()
+    q = torch.empty((m, k), dtype=torch.uint8, device="cuda:0")
+    s = torch.empty((m, k // 128), dtype=torch.float32, device="cuda:0")
+    assert inferop_amd.quant_fp8_per_token_group(q, s, x, getattr(DT, kind), m, k) == 0
+    qr, sr = oracle.quant(x.float().cpu().numpy())
+    _assert_same(to_np(q), to_np(s), qr, sr, f"{kind} {m}x{k} whole tensor")
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("out", ["fp32", "bf16", "fp16"])
 @pytest.mark.parametrize("gs", [128, 64, 48, 40, 36])  # 36: the element-wise path
 def test_dequant_parity(out, gs):
