@@ -254,3 +254,33 @@ def test_graph_fused_producers_replay_match_eager():
         torch.cuda.synchronize()
         for a, b in zip(outs["graph"], outs["eager"]):
             assert torch.equal(a, b), f"replay {rep}"
+
+
+@pytest.mark.gpu
+def test_graph_silu_fp16_lds_kernel_replay_match_eager():
+    # 256 tokens x 8192 outputs = 16384 groups: the fp16 kernel that copies
+    # a slice of the device's fp16 SiLU table into LDS; replays equal eager
+    device()
+    tokens, d = 256, 8192
+    g = torch.Generator(device="cuda:0").manual_seed(12)
+    gu = (torch.randn((tokens, 2 * d), generator=g, device="cuda:0") * 3).to(torch.float16)
+    st = torch.cuda.Stream()
+    q0 = torch.empty((tokens, d), dtype=torch.uint8, device="cuda:0")
+    s0 = torch.empty((tokens, d // 128), dtype=torch.float32, device="cuda:0")
+    q = torch.empty_like(q0)
+    s = torch.empty_like(s0)
+    with torch.cuda.stream(st):
+        assert inferop_amd.silu_and_mul_quant_fp8(q0, s0, gu, DT.fp16, tokens, d,
+                                                  stream=st.cuda_stream) == 0
+    st.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        assert inferop_amd.silu_and_mul_quant_fp8(q, s, gu, DT.fp16, tokens, d,
+                                                  stream=st.cuda_stream) == 0
+    for rep in range(3):
+        q.zero_()
+        s.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(q, q0) and torch.equal(s, s0), f"replay {rep}"
